@@ -1,0 +1,359 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Q4_K weight path.
+
+Default workload: the 3B-class decode set at M=1,
+36 layers with distinct seeded Q4_K weights, each layer
+  QKV    gemv_quant_triple  [2048 | 256 | 256] x 2048
+  O      gemv_quant_add     [2048 x 2048]   (+ fp16 residual)
+  gate+up gemv_quant_pair   [11008 | 11008] x 2048
+  down   gemv_quant_add     [2048 x 11008]  (+ fp16 residual)
+issued through the reflex::infer C++ API (weights_device set, as a runtime
+with resolved weight aliases does) on one stream and replayed as a HIP graph.
+A step is one pass over all 36 layers (144 launches); `value` is algorithmic
+bytes per step / seconds per step.  Inputs are resident in HBM; the 1.56 GB
+of weights exceed the 256 MB Infinity Cache, so every step streams from HBM.
+
+Also reported, each on the stream it runs on with HIP events:
+  roofline     the dominant kernel (gate+up pair GEMV), per-launch duration
+  per_kernel   every decode projection, the LM head [151936 x 2048] fp32
+               GEMV, the 4096-id Zipf(1.1) embedding gather, and the prefill
+               GEMM at m=512 (TFLOP/s, BASELINE metric's second half)
+  cpu_baseline the oracle's restatement of the reference CPU GEMV
+               (gemv_quant_cpu) over the full 36-layer set, single thread.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "reflex-infer_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+HIDDEN, FFN, N_LAYERS = 2048, 11008, 36
+QKV = (2048, 256, 256)
+VOCAB = 151936
+METRIC = "Q4_K GEMV HBM GB/s (% of peak) at M=1; Q4 GEMM TFLOP/s at M=512"
+
+
+def qbytes(rows: int, K: int) -> int:
+    return rows * (K // 256) * 144
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip LM head / embedding / GEMM")
+    ap.add_argument("--eager", action="store_true", help="time eager launches, not a graph")
+    return ap.parse_args()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the Q4_K kernels run on one MI355X; sharding is design-only). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import rxq4
+    from rxq4 import api, capi
+
+    rxq4.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+
+    def gen(seed: int, shape, sigma: float) -> torch.Tensor:
+        g = torch.Generator(device=dev).manual_seed(seed)
+        return torch.randn(shape, generator=g, device=dev) * sigma
+
+    def qweights(seed: int, rows: int, K: int) -> torch.Tensor:
+        src = gen(seed, (rows, K), 0.02)
+        w = capi.quantize(src)
+        del src
+        return w
+
+    # ------------------------------------------------------------- inputs
+    log("quantising 36 layers of Q4_K weights on the GPU")
+    layers = []
+    for l in range(N_LAYERS):
+        layers.append({
+            "qkv": qweights(10_000 + 10 * l + 0, sum(QKV), HIDDEN),
+            "o": qweights(10_000 + 10 * l + 1, HIDDEN, HIDDEN),
+            "gu": qweights(10_000 + 10 * l + 2, 2 * FFN, HIDDEN),
+            "down": qweights(10_000 + 10 * l + 3, HIDDEN, FFN),
+        })
+    x_h = gen(1, (HIDDEN,), 1.0).half()
+    x_a = gen(2, (HIDDEN,), 1.0).half()
+    x_f = gen(3, (FFN,), 1.0).half()
+    res = gen(4, (HIDDEN,), 1.0).half()
+    y_qkv = torch.empty(sum(QKV), dtype=torch.float16, device=dev)
+    y_o = torch.empty(HIDDEN, dtype=torch.float16, device=dev)
+    y_gu = torch.empty(2 * FFN, dtype=torch.float16, device=dev)
+    y_d = torch.empty(HIDDEN, dtype=torch.float16, device=dev)
+    torch.cuda.synchronize()
+
+    rb = qbytes(1, HIDDEN)
+    calls = []  # (api name, args struct) in issue order
+    for L in layers:
+        q = L["qkv"].data_ptr()
+        calls.append(("gemv_quant_triple", api.GemvQuantTripleArgs(
+            y0=y_qkv.data_ptr(), weights0=q, weights0_device=q, ggml_type0=12, M0=QKV[0],
+            y1=y_qkv.data_ptr() + 2 * QKV[0], weights1=q + QKV[0] * rb,
+            weights1_device=q + QKV[0] * rb, ggml_type1=12, M1=QKV[1],
+            y2=y_qkv.data_ptr() + 2 * (QKV[0] + QKV[1]),
+            weights2=q + (QKV[0] + QKV[1]) * rb, weights2_device=q + (QKV[0] + QKV[1]) * rb,
+            ggml_type2=12, M2=QKV[2], x=x_h.data_ptr(), K=HIDDEN, stream=sp)))
+        calls.append(("gemv_quant_add", api.GemvQuantAddArgs(
+            y=y_o.data_ptr(), weights=L["o"].data_ptr(), weights_device=L["o"].data_ptr(),
+            ggml_type=12, x=x_a.data_ptr(), residual=res.data_ptr(), M=HIDDEN, K=HIDDEN,
+            stream=sp)))
+        g = L["gu"].data_ptr()
+        calls.append(("gemv_quant_pair", api.GemvQuantPairArgs(
+            y0=y_gu.data_ptr(), weights0=g, weights0_device=g, ggml_type0=12, M0=FFN,
+            y1=y_gu.data_ptr() + 2 * FFN, weights1=g + FFN * rb, weights1_device=g + FFN * rb,
+            ggml_type1=12, M1=FFN, x=x_h.data_ptr(), K=HIDDEN, stream=sp)))
+        calls.append(("gemv_quant_add", api.GemvQuantAddArgs(
+            y=y_d.data_ptr(), weights=L["down"].data_ptr(),
+            weights_device=L["down"].data_ptr(), ggml_type=12, x=x_f.data_ptr(),
+            residual=res.data_ptr(), M=HIDDEN, K=FFN, stream=sp)))
+    fns = {name: api._fn(name) for name in {c[0] for c in calls}}
+    import ctypes
+    bound = [(fns[n], ctypes.byref(a)) for n, a in calls]
+
+    def step():
+        for f, a in bound:
+            s = f(a)
+            if s != 0:
+                raise RuntimeError(f"API call failed with status {s}: {capi.last_error()}")
+
+    # algorithmic bytes of one step
+    step_bytes = 0
+    step_bytes += N_LAYERS * (qbytes(sum(QKV), HIDDEN) + 2 * HIDDEN + 2 * sum(QKV))
+    step_bytes += N_LAYERS * (qbytes(HIDDEN, HIDDEN) + 2 * HIDDEN + 2 * HIDDEN + 2 * HIDDEN)
+    step_bytes += N_LAYERS * (qbytes(2 * FFN, HIDDEN) + 2 * HIDDEN + 2 * 2 * FFN)
+    step_bytes += N_LAYERS * (qbytes(HIDDEN, FFN) + 2 * FFN + 2 * HIDDEN + 2 * HIDDEN)
+
+    with torch.cuda.stream(stream):
+        step()  # eager warm-up (also caches device properties)
+    torch.cuda.synchronize()
+
+    graph = None
+    if not args.eager:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream, capture_error_mode="relaxed"):
+            step()
+        torch.cuda.synchronize()
+
+    def run_once():
+        if graph is not None:
+            graph.replay()
+        else:
+            step()
+
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            run_once()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(args.steps):
+            run_once()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = wall * 1e3 / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"decode36: {ms_per_step:.3f} ms/step (events {gpu_ms / args.steps:.3f}), "
+        f"{value:.1f} GB/s = {100 * value / HBM_PEAK_GBS:.1f}% of 8 TB/s")
+
+    # eager time for reference
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / 3
+
+    # ------------------------------------------------ per-kernel durations
+    def per_launch(launch, n, warm=3):
+        """Mean duration of `launch(i)` bracketed by events on `stream`."""
+        with torch.cuda.stream(stream):
+            for i in range(warm):
+                launch(i)
+        torch.cuda.synchronize()
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        with torch.cuda.stream(stream):
+            for i in range(n):
+                starts[i].record(stream)
+                launch(i)
+                ends[i].record(stream)
+        torch.cuda.synchronize()
+        d = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))  # us
+        return float(np.median(d)), float(np.mean(d))
+
+    kernels = {}
+    R = 72
+    rows_multi = lambda ws: [(w[0], w[1], w[2]) for w in ws]  # noqa: E731
+
+    def gu_launch(i):
+        L = layers[i % N_LAYERS]
+        g = L["gu"]
+        capi.gemv_multi_f16([(y_gu[:FFN], g[:FFN], FFN), (y_gu[FFN:], g[FFN:], FFN)], x_h,
+                            HIDDEN, stream=sp)
+
+    med, mean = per_launch(gu_launch, R)
+    gu_bytes = qbytes(2 * FFN, HIDDEN) + 2 * HIDDEN + 2 * 2 * FFN
+    kernels["gate_up_pair_22016x2048"] = {"us": round(med, 3), "GBps": round(gu_bytes / med / 1e3, 1)}
+    roofline = {"bound": "hbm", "achieved": round(gu_bytes / med / 1e3, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(gu_bytes / med / 1e3 / HBM_PEAK_GBS, 4),
+                "traffic": None, "kernel": "gemv_reg_kernel<32,F16> (gate+up pair)",
+                "bytes_per_launch": gu_bytes, "us_per_launch": round(med, 3),
+                "us_mean": round(mean, 3)}
+
+    def qkv_launch(i):
+        q = layers[i % N_LAYERS]["qkv"]
+        capi.gemv_multi_f16([(y_qkv[:2048], q[:2048], 2048), (y_qkv[2048:2304], q[2048:2304], 256),
+                             (y_qkv[2304:], q[2304:], 256)], x_h, HIDDEN, stream=sp)
+    med, _ = per_launch(qkv_launch, R)
+    b = qbytes(2560, HIDDEN) + 2 * HIDDEN + 2 * 2560
+    kernels["qkv_triple_2560x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+
+    def o_launch(i):
+        capi.gemv_add_f16(y_o, layers[i % N_LAYERS]["o"], x_a, res, HIDDEN, HIDDEN, stream=sp)
+    med, _ = per_launch(o_launch, R)
+    b = qbytes(HIDDEN, HIDDEN) + 6 * HIDDEN
+    kernels["o_add_2048x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+
+    def d_launch(i):
+        capi.gemv_add_f16(y_d, layers[i % N_LAYERS]["down"], x_f, res, HIDDEN, FFN, stream=sp)
+    med, _ = per_launch(d_launch, R)
+    b = qbytes(HIDDEN, FFN) + 2 * FFN + 4 * HIDDEN
+    kernels["down_add_2048x11008"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+
+    extras = {}
+    if not args.no_extras:
+        # LM head: two tables (350 MB > 256 MB Infinity Cache), alternate.
+        log("LM head / embedding / GEMM extras")
+        heads = [qweights(20_000 + i, VOCAB, HIDDEN) for i in range(2)]
+        logits = torch.empty(VOCAB, dtype=torch.float32, device=dev)
+
+        def lm_launch(i):
+            capi.gemv_f32(logits, heads[i % 2], x_h, VOCAB, HIDDEN, stream=sp)
+        med, _ = per_launch(lm_launch, 20)
+        b = qbytes(VOCAB, HIDDEN) + 2 * HIDDEN + 4 * VOCAB
+        kernels["lm_head_f32_151936x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+
+        # Embedding gather: 4096 Zipf(1.1) ids over the vocabulary.
+        rng = np.random.default_rng(5)
+        ranks = np.arange(1, VOCAB + 1, dtype=np.float64)
+        cdf = np.cumsum(ranks ** -1.1)
+        cdf /= cdf[-1]
+        perm = rng.permutation(VOCAB)
+        ids_np = perm[np.minimum(np.searchsorted(cdf, rng.random(4096)), VOCAB - 1)].astype(np.int32)
+        ids = torch.from_numpy(ids_np).to(dev)
+        emb = torch.empty((4096, HIDDEN), dtype=torch.float16, device=dev)
+
+        def emb_launch(i):
+            capi.embed_rows_f16(emb, heads[i % 2], VOCAB, ids, HIDDEN, stream=sp)
+        med, _ = per_launch(emb_launch, 20)
+        uniq = int(np.unique(ids_np).size)
+        b = uniq * qbytes(1, HIDDEN) + 4096 * HIDDEN * 2 + 4096 * 4
+        kernels["embed_gather_4096_zipf"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
+                                             "unique_rows": uniq}
+        del heads
+
+        # Prefill GEMM at m = 512 (bf16 activations, bf16 out).
+        for (M, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):
+            ws = [qweights(30_000 + M + i, M, K) for i in range(4)]
+            xb = gen(40_000 + K, (512, K), 1.0).to(torch.bfloat16)
+            yb = torch.empty((512, M), dtype=torch.bfloat16, device=dev)
+
+            def gm_launch(i):
+                capi.gemm(yb, ws[i % 4], xb, M, 512, K, stream=sp)
+            med, _ = per_launch(gm_launch, 20)
+            tf = 2 * 512 * M * K / med / 1e6
+            kernels[f"gemm_bf16_m512_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1),
+                                                  "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            del ws
+        extras["gemm_m512_tflops"] = min(v["TFLOPs"] for k, v in kernels.items()
+                                         if k.startswith("gemm_bf16_m512"))
+
+    # ------------------------------------------------------- CPU baseline
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+        log("CPU baseline: oracle restatement of gemv_quant_cpu over 36 layers, 1 thread")
+        xs = {HIDDEN: x_h.cpu().numpy().view(np.uint16), FFN: x_f.cpu().numpy().view(np.uint16)}
+        hostw = [{k: v.cpu().numpy() for k, v in L.items()} for L in layers]
+        t0 = time.perf_counter()
+        for L in hostw:
+            orc.gemv_f32(L["qkv"], HIDDEN, xs[HIDDEN])
+            orc.gemv_f32(L["o"], HIDDEN, xs[HIDDEN])
+            orc.gemv_f32(L["gu"], HIDDEN, xs[HIDDEN])
+            orc.gemv_f32(L["down"], FFN, xs[FFN])
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(step_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": "full 36-layer decode set (one step), fp32 outputs, single thread; "
+                         f"{cpu_s:.2f} s",
+               "ms_per_step": round(cpu_s * 1e3, 1)}
+        log(f"CPU baseline {cpu['value']} GB/s ({cpu_s:.2f} s per step)")
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode36: 36 layers x {QKV triple [2048|256|256]x2048, O add "
+                        "[2048x2048], gate+up pair [11008|11008]x2048, down add [2048x11008]}, "
+                        "Q4_K N(0,0.02) weights, fp16 N(0,1) activations, M=1, fp32 acc, fp16 out",
+            "launches_per_step": len(calls),
+            "bytes_per_step": step_bytes,
+            "issue": "eager" if graph is None else "hip_graph",
+        },
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "eager_ms_per_step": round(eager_ms, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_kernel": kernels,
+    }
+    out.update(extras)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,120 @@
+/*
+ * rxq4.h -- C ABI of the MI355X (gfx950) Q4_K weight-path library.
+ *
+ * Plain C: pointers, sizes and int status codes, no C++ or torch types.  The
+ * first seven entry points replace, one for one, the kernel-layer functions
+ * that reflex-infer's dispatcher binds (reference
+ * src/kernels/kernel_entrypoints.h:7-13, defined in src/kernels/q4_gemm.cu);
+ * the C++ API of include/reflex/infer.h is implemented on top of them.  The
+ * entry points marked NEW have no reference counterpart: they expose work
+ * the reference API cannot express (bf16 GEMM, batched embedding gather,
+ * small-batch decode, the quantiser used to build inputs).
+ *
+ * Conventions for every entry point:
+ *   - `w` is a DEVICE pointer to raw GGML Q4_K blocks (ggml_type 12): rows of
+ *     K/256 blocks of 144 bytes, row-major, 16-byte aligned.  Pointer
+ *     resolution of host/mmap pointers happens above this layer
+ *     (rxq4_resolve_weights).
+ *   - fp16/bf16 buffers are raw 16-bit patterns; x must be 16-byte aligned.
+ *   - K must be a positive multiple of 256 and at most RXQ4_MAX_K.
+ *   - `stream` is a hipStream_t (NULL = null stream).  Calls only enqueue
+ *     work; nothing synchronises and nothing allocates device memory.
+ *   - The return value is a reflex::infer::Status value (RXQ4_STATUS_*).
+ *     On an error nothing is launched; rxq4_last_error() says why.
+ */
+#ifndef RXQ4_H
+#define RXQ4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Values of reflex::infer::Status (reference include/reflex/infer.h:16-23). */
+#define RXQ4_STATUS_SUCCESS 0
+#define RXQ4_STATUS_UNSUPPORTED_DEVICE 1
+#define RXQ4_STATUS_UNSUPPORTED_MODEL 2
+#define RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT 3
+#define RXQ4_STATUS_INVALID_ARGUMENT 4
+#define RXQ4_STATUS_NOT_IMPLEMENTED 5
+
+#define RXQ4_GGML_TYPE_Q4_K 12
+#define RXQ4_MAX_K 65536
+
+/* Element types for the typed GEMM entry point. */
+#define RXQ4_DTYPE_F32 0
+#define RXQ4_DTYPE_F16 1
+#define RXQ4_DTYPE_BF16 2
+
+/* One output range of a multi-matrix GEMV sharing one x (pair = 2, triple = 3). */
+typedef struct rxq4_rows {
+    void *y;           /* fp16 [M] */
+    const void *w;     /* device Q4_K blocks [M x K/256] */
+    int ggml_type;
+    int M;
+} rxq4_rows;
+
+/* y[M] fp16 = RNE(W[M x K] . x[K]), fp32 accumulation.
+ * Replaces kernels::gemv_quant (reference q4_gemm.cu:2031-2036, 1856-1914). */
+int rxq4_gemv_f16(void *y, const void *w, int ggml_type, const void *x, int M, int K,
+                  void *stream);
+
+/* y[M] fp16 = RNE(float(RNE(W . x)) + float(residual)); y may equal residual.
+ * Replaces kernels::gemv_quant_add (reference q4_gemm.cu:2038-2045, 755-779). */
+int rxq4_gemv_add_f16(void *y, const void *w, int ggml_type, const void *x,
+                      const void *residual, int M, int K, void *stream);
+
+/* 1..3 independent GEMVs sharing x, one launch.
+ * Replaces kernels::gemv_quant_pair (reference q4_gemm.cu:2047-2056) with
+ * n_ranges = 2 and kernels::gemv_quant_triple (q4_gemm.cu:2058-2069) with 3. */
+int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, int K,
+                        void *stream);
+
+/* y[M] fp32 = W . x (logits).
+ * Replaces kernels::gemv_quant_f32 (reference q4_gemm.cu:2071-2076, 491-507). */
+int rxq4_gemv_f32(float *y, const void *w, int ggml_type, const void *x, int M, int K,
+                  void *stream);
+
+/* y[N x M] fp16 (token-major) = x[N x K] fp16 . W^T.  N == 1 is the GEMV;
+ * small N uses the multi-token GEMV kernel, large N the MFMA GEMM.
+ * Replaces kernels::gemm_quant_batched (reference q4_gemm.cu:2023-2029,
+ * 1707-1740). */
+int rxq4_gemm_f16(void *y, const void *w, int ggml_type, const void *x, int M, int N,
+                  int K, void *stream);
+
+/* dst[hidden] fp16 = dequant(W[token_id, :]), bit-exact.
+ * Replaces kernels::dequant_embedding_row (reference q4_gemm.cu:2078-2115).
+ * Like the reference, token_id is not range-checked (no vocab size given). */
+int rxq4_embed_row_f16(void *dst, const void *w, int ggml_type, int token_id,
+                       int hidden_dim, void *stream);
+
+/* NEW.  Typed GEMM: y[N x M] (y_dtype) = x[N x K] (x_dtype) . W^T.
+ * Supported: x F16 -> y F16|F32, x BF16 -> y BF16|F32.  Weight tiles are
+ * dequantised to the x type, products accumulate in fp32. */
+int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
+              int x_dtype, int M, int N, int K, void *stream);
+
+/* NEW.  Batched gather: dst[i, :] fp16 = dequant(W[ids[i], :]) for i < n_ids.
+ * ids is a device int32 array; ids outside [0, n_vocab) give a zero row. */
+int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab,
+                        const int32_t *ids, int n_ids, int hidden_dim, void *stream);
+
+/* NEW.  Quantise fp32 rows [n_rows x K] (device) to Q4_K blocks (device). */
+int rxq4_quantize_q4k(void *dst, const float *src, int64_t n_rows, int K, void *stream);
+
+/* Pointer resolution of the reference (q4_gemm.cu:111-135): returns
+ * w_device if non-NULL, else w if the HIP runtime reports it as device or
+ * managed memory, else NULL (host-only memory cannot be read by the kernels). */
+const void *rxq4_resolve_weights(const void *w, const void *w_device);
+
+/* Library version and the reason for the last non-success status on the
+ * calling thread ("" if none). */
+const char *rxq4_version(void);
+const char *rxq4_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,173 @@
+// embed_q4k.hip -- Q4_K embedding-row dequantisation for gfx950.
+//
+// Replaces dequant_embedding_q4k_kernel (reference q4_gemm.cu:545-572) and
+// adds the batched gather the reference API cannot express.  A thread owns 8
+// consecutive outputs of one row: it reads the 16-byte block header and 8
+// quant bytes, computes w = (d*sc)*q - dmin*m in fp32 (one rounding, as the
+// reference) and writes 8 fp16 (RNE) values with one 16-byte store.  Only the
+// addressed rows are read.  Bytes per launch: unique_rows*K/256*144 (header
+// reads are L2 hits after the first) + n_ids*K*2 written + n_ids*4 ids.
+#include "launch.h"
+#include "q4k_device.h"
+
+namespace rxq4 {
+
+template <bool kBatched>
+__global__ __launch_bounds__(256) void embed_kernel(uint16_t *__restrict__ dst,
+                                                    const uint8_t *__restrict__ w,
+                                                    const int32_t *__restrict__ ids,
+                                                    int token_id, int64_t n_vocab,
+                                                    int n_ids, int K) {
+    const int per_row = K >> 3;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = t / per_row;
+    const int c = (int)(t - i * per_row);
+    if (i >= n_ids) return;
+    u32x4 *out = reinterpret_cast<u32x4 *>(dst + i * K + c * 8);
+    int64_t id = token_id;
+    if (kBatched) {
+        id = ids[i];
+        if (id < 0 || id >= n_vocab) {
+            *out = u32x4{0, 0, 0, 0};
+            return;
+        }
+    }
+    const int nb = K >> 8;
+    const int e0 = c * 8;
+    const int b = e0 >> 8;
+    const int pos = e0 & 255;
+    const int il = pos >> 6;
+    const int hi = (pos >> 5) & 1;
+    const int l0 = pos & 31;
+    const uint8_t *blk = w + (id * nb + b) * kBlockBytes;
+    const u32x4 h = load16(blk);
+    const u32x2 q = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * il + l0);
+    const float d = f16_bits_to_f32(h.x & 0xFFFFu);
+    const float dmin = f16_bits_to_f32(h.x >> 16);
+    uint32_t sc, mn;
+    scale_one(h.y, h.z, h.w, 2 * il + hi, &sc, &mn);
+    const float ds = d * (float)sc;
+    const float dm = dmin * (float)mn;
+    uint32_t packed[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t word = j < 2 ? q.x : q.y;
+        const int sh0 = (2 * j & 3) * 8, sh1 = sh0 + 8;
+        uint32_t b0 = (word >> sh0) & 0xFFu, b1 = (word >> sh1) & 0xFFu;
+        b0 = hi ? (b0 >> 4) : (b0 & 0xFu);
+        b1 = hi ? (b1 >> 4) : (b1 & 0xFu);
+        const float v0 = ds * (float)b0 - dm;
+        const float v1 = ds * (float)b1 - dm;
+        packed[j] = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
+    }
+    *out = u32x4{packed[0], packed[1], packed[2], packed[3]};
+}
+
+hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
+                        int64_t n_vocab, int n_ids, int K, hipStream_t st) {
+    const int64_t threads = (int64_t)n_ids * (K >> 3);
+    const int64_t grid = (threads + 255) / 256;
+    if (grid <= 0) return hipSuccess;
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+    if (ids)
+        embed_kernel<true><<<(unsigned)grid, 256, 0, st>>>(dst, w, ids, 0, n_vocab, n_ids, K);
+    else
+        embed_kernel<false><<<(unsigned)grid, 256, 0, st>>>(dst, w, nullptr, token_id, 0, 1, K);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Quantiser (the reference ships none): one wave per 256-value block, four
+// values per lane, eight lanes per 32-value sub-block.  Same arithmetic, in the
+// same order, as the oracle's quantize_block; only min/max, +, *, correctly
+// rounded / and rint are used, so the bytes are identical.
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void quantize_kernel(uint8_t *__restrict__ dst,
+                                                       const float *__restrict__ src,
+                                                       int64_t n_blocks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= n_blocks) return;
+    const float *v = src + blk * kQK + lane * 4;
+    const float x0 = v[0], x1 = v[1], x2 = v[2], x3 = v[3];
+    float lo = x0, hi = x0;
+    lo = x1 < lo ? x1 : lo; hi = x1 > hi ? x1 : hi;
+    lo = x2 < lo ? x2 : lo; hi = x2 > hi ? x2 : hi;
+    lo = x3 < lo ? x3 : lo; hi = x3 > hi ? x3 : hi;
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        const float ol = __shfl_xor(lo, off, 64), oh = __shfl_xor(hi, off, 64);
+        lo = ol < lo ? ol : lo;
+        hi = oh > hi ? oh : hi;
+    }
+    const float mo = lo < 0.0f ? -lo : 0.0f;
+    const float top = hi > 0.0f ? hi : 0.0f;
+    const float span = (top + mo) / 15.0f;
+    float max_span = span, max_off = mo;
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        const float os = __shfl_xor(max_span, off, 64), oo = __shfl_xor(max_off, off, 64);
+        max_span = os > max_span ? os : max_span;
+        max_off = oo > max_off ? oo : max_off;
+    }
+    const uint16_t d_raw = f32_to_f16_bits(max_span / 63.0f);
+    const uint16_t dmin_raw = f32_to_f16_bits(max_off / 63.0f);
+    const float d = f16_bits_to_f32(d_raw);
+    const float dmin = f16_bits_to_f32(dmin_raw);
+    float scf = 0.0f, mnf = 0.0f;
+    if (d > 0.0f) scf = fminf(fmaxf(rintf(span / d), 0.0f), 63.0f);
+    if (dmin > 0.0f) mnf = fminf(fmaxf(rintf(mo / dmin), 0.0f), 63.0f);
+    const float step = d * scf;
+    const float bias = dmin * mnf;
+    const float xs[4] = {x0, x1, x2, x3};
+    uint32_t qpack = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float qv = 0.0f;
+        if (step > 0.0f) qv = fminf(fmaxf(rintf((xs[i] + bias) / step), 0.0f), 15.0f);
+        qpack |= ((uint32_t)qv) << (8 * i);
+    }
+    uint8_t *out = dst + blk * kBlockBytes;
+    // Element e = 4*lane + i sits in sub-block j = lane / 8.  Byte
+    // qs[32*il + l] = q[64*il + l] | q[64*il + 32 + l] << 4: lanes of even
+    // sub-blocks combine with the lane 8 above.
+    const uint32_t upper = __shfl(qpack, (lane + 8) & 63, 64);
+    const int j = lane >> 3;
+    if ((j & 1) == 0) {
+        const int il = j >> 1;
+        *reinterpret_cast<uint32_t *>(out + 16 + 32 * il + (4 * lane - 64 * il)) =
+            qpack | (upper << 4);
+    }
+    // Header: gather the eight (sc, m) pairs and pack them (GGML layout).
+    const uint32_t scu = (uint32_t)scf, mnu = (uint32_t)mnf;
+    uint32_t sc[8], mn[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        sc[s] = __shfl(scu, 8 * s, 64);
+        mn[s] = __shfl(mnu, 8 * s, 64);
+    }
+    if (lane == 0) {
+        uint32_t words[3] = {0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const uint32_t b0 = (sc[s] & 63u) | ((sc[s + 4] >> 4) << 6);
+            const uint32_t b4 = (mn[s] & 63u) | ((mn[s + 4] >> 4) << 6);
+            const uint32_t b8 = (sc[s + 4] & 0xFu) | ((mn[s + 4] & 0xFu) << 4);
+            words[0] |= b0 << (8 * s);
+            words[1] |= b4 << (8 * s);
+            words[2] |= b8 << (8 * s);
+        }
+        *reinterpret_cast<u32x4 *>(out) =
+            u32x4{(uint32_t)d_raw | ((uint32_t)dmin_raw << 16), words[0], words[1], words[2]};
+    }
+}
+
+hipError_t launch_quantize(uint8_t *dst, const float *src, int64_t n_blocks, hipStream_t st) {
+    const int64_t grid = (n_blocks + 3) / 4;
+    if (grid <= 0) return hipSuccess;
+    if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+    quantize_kernel<<<(unsigned)grid, 256, 0, st>>>(dst, src, n_blocks);
+    return hipGetLastError();
+}
+
+}  // namespace rxq4

@@ -1,0 +1,61 @@
+// launch.h -- host-side launchers of the gfx950 kernels (internal; the public
+// surface is the C ABI in include/rxq4.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rxq4 {
+
+enum Epilogue : int { kEpiF16 = 0, kEpiF32 = 1, kEpiAdd = 2 };
+
+// One output range of a (multi-)GEMV: rows of `w` produce y[0 .. rows).
+struct GemvRange {
+    const uint8_t *w;
+    void *y;
+    const uint16_t *res;  // fp16 residual, kEpiAdd only
+    int rows;
+};
+
+struct GemvParams {
+    GemvRange r[3];
+    int n_ranges;
+    int total_rows;
+    const uint16_t *x;  // fp16 [K], 16-byte aligned
+    int nb;             // Q4_K blocks per row = K / 256
+    int rows_per_unit;  // rows per wave (register kernel) or per workgroup (split kernel)
+};
+
+struct DeviceInfo {
+    int cu_count;
+    int arch_ok;  // 1 if the current device is gfx950
+};
+
+// Cached properties of the current device.
+const DeviceInfo &device_info();
+
+// Launch a GEMV over 1..3 ranges with the given epilogue.  Shapes were
+// validated by the caller.  Returns hipSuccess or the launch error.
+hipError_t launch_gemv(GemvParams p, int epilogue, hipStream_t stream);
+
+// Multi-token GEMV for 2 <= n_tok <= kMaxSmallBatch tokens:
+// y[t*M + row] (fp16 or fp32) = W[row] . x[t].
+constexpr int kMaxSmallBatch = 16;
+hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void *x,
+                              int x_dtype, int M, int n_tok, int K, hipStream_t stream);
+
+// MFMA GEMM: y[N x M] = x[N x K] . dequant(W)^T with x/weight tiles of the
+// x type (fp16 or bf16) and fp32 accumulation; y fp32/fp16/bf16.
+hipError_t launch_gemm(void *y, int y_dtype, const uint8_t *w, const void *x, int x_dtype,
+                       int M, int N, int K, hipStream_t stream);
+
+// Embedding rows: dst[i, :] = fp16(dequant(W[id_i, :])).  ids == nullptr means
+// the single row token_id (no range check, as in the reference).
+hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
+                        int64_t n_vocab, int n_ids, int K, hipStream_t stream);
+
+// fp32 rows -> Q4_K blocks.
+hipError_t launch_quantize(uint8_t *dst, const float *src, int64_t n_blocks,
+                           hipStream_t stream);
+
+}  // namespace rxq4

@@ -1,0 +1,89 @@
+// q4k_device.h -- Q4_K block format and device helpers shared by the gfx950
+// kernels.
+//
+// GGUF Q4_K super-block (reference q4_gemm.cu:147-154): 256 weights in 144
+// bytes = 9 aligned 16-byte chunks.
+//   bytes  0..1   d     fp16 super-block scale
+//   bytes  2..3   dmin  fp16 super-block min
+//   bytes  4..15  scales[12]: eight 6-bit (sc, m) pairs, GGML packing
+//                 (unpacked by get_scale_min_k4, q4_gemm.cu:192-202)
+//   bytes 16..143 qs[128]: byte 32*il + l holds element 64*il + l in its low
+//                 nibble and element 64*il + 32 + l in its high nibble
+// Element value: w = d*sc[s]*q - dmin*m[s], s = sub-block (32 elements).
+// d*sc and (d*sc)*q and dmin*m are exact in fp32, so w has exactly one
+// rounding whatever the evaluation order or FMA contraction.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rxq4 {
+
+constexpr int kQK = 256;
+constexpr int kBlockBytes = 144;
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, (_Float16)v);  // v_cvt_f16_f32, RNE
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+    return __builtin_bit_cast(float, bits16 << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
+    return __builtin_bit_cast(uint16_t, (__bf16)v);  // RNE
+}
+
+__device__ __forceinline__ half2_t as_half2(uint32_t v) {
+    return __builtin_bit_cast(half2_t, v);
+}
+
+// 16-byte global load through the vector memory path.
+__device__ __forceinline__ u32x4 load16(const void *p) {
+    return *reinterpret_cast<const u32x4 *>(p);
+}
+
+// The (sc, m) pairs of sub-blocks 2*il and 2*il+1 from the three scale dwords
+// s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].  Returns
+// sc_lo | sc_hi << 8 in *sc and m_lo | m_hi << 8 in *mn.  Same values as
+// get_scale_min_k4(2*il) / get_scale_min_k4(2*il+1).
+__device__ __forceinline__ void scale_pair(uint32_t s0, uint32_t s1, uint32_t s2, int il,
+                                           uint32_t *sc, uint32_t *mn) {
+    const int sh = (il & 1) << 4;
+    const uint32_t a = s0 >> sh, b = s1 >> sh, c = s2 >> sh;
+    if (il < 2) {
+        *sc = a & 0x3F3Fu;
+        *mn = b & 0x3F3Fu;
+    } else {
+        *sc = (c & 0x0F0Fu) | ((a >> 2) & 0x3030u);
+        *mn = ((c >> 4) & 0x0F0Fu) | ((b >> 2) & 0x3030u);
+    }
+}
+
+// The (sc, m) pair of one sub-block j in [0, 8).
+__device__ __forceinline__ void scale_one(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                          uint32_t *sc, uint32_t *mn) {
+    uint32_t p, q;
+    scale_pair(s0, s1, s2, j >> 1, &p, &q);
+    const int sh = (j & 1) << 3;
+    *sc = (p >> sh) & 0xFFu;
+    *mn = (q >> sh) & 0xFFu;
+}
+
+// Sum over the lanes of aligned groups of `width` lanes (power of two <= 64).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace rxq4

@@ -1,0 +1,249 @@
+// rxq4_capi.hip -- the C ABI (include/rxq4.h) over the gfx950 launchers.
+//
+// Each entry point validates its arguments on the host, then enqueues on the
+// caller's stream.  No entry point allocates, synchronises or falls back to
+// the CPU: a call either launches the HIP kernels or returns a non-success
+// status with the reason in rxq4_last_error().
+#include "rxq4.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "launch.h"
+
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+int fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int ok() {
+    g_last_error[0] = '\0';
+    return RXQ4_STATUS_SUCCESS;
+}
+
+int from_hip(hipError_t e, const char *what) {
+    if (e == hipSuccess) return ok();
+    return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: HIP error %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks shared by every weight-streaming entry point.
+int check_common(const char *fn, const void *w, int ggml_type, int K) {
+    if (ggml_type != RXQ4_GGML_TYPE_Q4_K)
+        return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT,
+                    "%s: ggml_type %d not supported (only Q4_K = 12)", fn, ggml_type);
+    if (K <= 0 || K % 256 != 0 || K > RXQ4_MAX_K)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT,
+                    "%s: K=%d must be a positive multiple of 256 and <= %d", fn, K, RXQ4_MAX_K);
+    if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weight pointer", fn);
+    if (!aligned16(w))
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights must be 16-byte aligned", fn);
+    return RXQ4_STATUS_SUCCESS;
+}
+
+// Last check before a launch (the only one that queries the HIP runtime).
+int check_device(const char *fn) {
+    if (!rxq4::device_info().arch_ok)
+        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+    return RXQ4_STATUS_SUCCESS;
+}
+
+int check_x(const char *fn, const void *x) {
+    if (!x) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null x", fn);
+    if (!aligned16(x)) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: x must be 16-byte aligned", fn);
+    return RXQ4_STATUS_SUCCESS;
+}
+
+int gemv_single(const char *fn, void *y, const void *w, int ggml_type, const void *x,
+                const void *residual, int M, int K, int epi, void *stream) {
+    int s = check_common(fn, w, ggml_type, K);
+    if (s != RXQ4_STATUS_SUCCESS) return s;
+    if ((s = check_x(fn, x)) != RXQ4_STATUS_SUCCESS) return s;
+    if (M < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: M=%d < 0", fn, M);
+    if (M == 0) return ok();
+    if (!y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null y", fn);
+    if (epi == rxq4::kEpiAdd && !residual)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null residual", fn);
+    if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
+    rxq4::GemvParams p{};
+    p.r[0] = rxq4::GemvRange{static_cast<const uint8_t *>(w), y,
+                             static_cast<const uint16_t *>(residual), M};
+    p.n_ranges = 1;
+    p.total_rows = M;
+    p.x = static_cast<const uint16_t *>(x);
+    p.nb = K / 256;
+    return from_hip(rxq4::launch_gemv(p, epi, static_cast<hipStream_t>(stream)), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rxq4_gemv_f16(void *y, const void *w, int ggml_type, const void *x, int M, int K,
+                  void *stream) {
+    return gemv_single("rxq4_gemv_f16", y, w, ggml_type, x, nullptr, M, K, rxq4::kEpiF16,
+                       stream);
+}
+
+int rxq4_gemv_f32(float *y, const void *w, int ggml_type, const void *x, int M, int K,
+                  void *stream) {
+    return gemv_single("rxq4_gemv_f32", y, w, ggml_type, x, nullptr, M, K, rxq4::kEpiF32,
+                       stream);
+}
+
+int rxq4_gemv_add_f16(void *y, const void *w, int ggml_type, const void *x,
+                      const void *residual, int M, int K, void *stream) {
+    return gemv_single("rxq4_gemv_add_f16", y, w, ggml_type, x, residual, M, K,
+                       rxq4::kEpiAdd, stream);
+}
+
+int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, int K,
+                        void *stream) {
+    const char *fn = "rxq4_gemv_multi_f16";
+    if (!ranges || n_ranges < 1 || n_ranges > 3)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ranges=%d must be 1..3", fn, n_ranges);
+    rxq4::GemvParams p{};
+    int64_t total = 0;
+    for (int i = 0; i < n_ranges; ++i) {
+        const rxq4_rows &r = ranges[i];
+        int s = check_common(fn, r.w, r.ggml_type, K);
+        if (s != RXQ4_STATUS_SUCCESS) return s;
+        if (r.M < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d M=%d < 0", fn, i, r.M);
+        if (r.M > 0 && !r.y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d null y", fn, i);
+        p.r[i] = rxq4::GemvRange{static_cast<const uint8_t *>(r.w), r.y, nullptr, r.M};
+        total += r.M;
+    }
+    int s = check_x(fn, x);
+    if (s != RXQ4_STATUS_SUCCESS) return s;
+    if (total > 0x7FFFFFFF) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: too many rows", fn);
+    if (total == 0) return ok();
+    if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
+    p.n_ranges = n_ranges;
+    p.total_rows = (int)total;
+    p.x = static_cast<const uint16_t *>(x);
+    p.nb = K / 256;
+    return from_hip(rxq4::launch_gemv(p, rxq4::kEpiF16, static_cast<hipStream_t>(stream)), fn);
+}
+
+int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x, int x_dtype,
+              int M, int N, int K, void *stream) {
+    const char *fn = "rxq4_gemm";
+    int s = check_common(fn, w, ggml_type, K);
+    if (s != RXQ4_STATUS_SUCCESS) return s;
+    if ((s = check_x(fn, x)) != RXQ4_STATUS_SUCCESS) return s;
+    if (M < 0 || N < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: M=%d N=%d", fn, M, N);
+    if (M == 0 || N == 0) return ok();
+    if (!y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null y", fn);
+    const bool f16_ok = x_dtype == RXQ4_DTYPE_F16 &&
+                        (y_dtype == RXQ4_DTYPE_F16 || y_dtype == RXQ4_DTYPE_F32);
+    const bool bf16_ok = x_dtype == RXQ4_DTYPE_BF16 &&
+                         (y_dtype == RXQ4_DTYPE_BF16 || y_dtype == RXQ4_DTYPE_F32);
+    if (!f16_ok && !bf16_ok)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: unsupported dtypes x=%d y=%d", fn,
+                    x_dtype, y_dtype);
+    if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (N == 1 && x_dtype == RXQ4_DTYPE_F16) {
+        // One token is the decode GEMV (reference q4_gemm.cu:1714-1717).
+        return gemv_single(fn, y, w, ggml_type, x, nullptr, M, K,
+                           y_dtype == RXQ4_DTYPE_F32 ? rxq4::kEpiF32 : rxq4::kEpiF16, stream);
+    }
+    hipError_t e;
+    if (N <= rxq4::kMaxSmallBatch)
+        e = rxq4::launch_gemv_tokens(y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M,
+                                     N, K, st);
+    else
+        e = rxq4::launch_gemm(y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M, N, K,
+                              st);
+    return from_hip(e, fn);
+}
+
+int rxq4_gemm_f16(void *y, const void *w, int ggml_type, const void *x, int M, int N, int K,
+                  void *stream) {
+    return rxq4_gemm(y, RXQ4_DTYPE_F16, w, ggml_type, x, RXQ4_DTYPE_F16, M, N, K, stream);
+}
+
+int rxq4_embed_row_f16(void *dst, const void *w, int ggml_type, int token_id, int hidden_dim,
+                       void *stream) {
+    const char *fn = "rxq4_embed_row_f16";
+    // Order of checks as the reference (q4_gemm.cu:2079-2105): shape first,
+    // then the weight pointer, then the type.
+    if (hidden_dim <= 0 || hidden_dim % 256 != 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
+    if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
+    if (ggml_type != RXQ4_GGML_TYPE_Q4_K)
+        return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
+    if (!aligned16(w) || !dst || !aligned16(dst))
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights/dst must be 16-byte aligned", fn);
+    if (!rxq4::device_info().arch_ok)
+        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+    return from_hip(rxq4::launch_embed(static_cast<uint16_t *>(dst),
+                                       static_cast<const uint8_t *>(w), nullptr, token_id, 0, 1,
+                                       hidden_dim, static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab,
+                        const int32_t *ids, int n_ids, int hidden_dim, void *stream) {
+    const char *fn = "rxq4_embed_rows_f16";
+    if (hidden_dim <= 0 || hidden_dim % 256 != 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
+    if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
+    if (ggml_type != RXQ4_GGML_TYPE_Q4_K)
+        return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
+    if (n_ids < 0 || n_vocab < 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ids=%d n_vocab=%lld", fn, n_ids,
+                    (long long)n_vocab);
+    if (n_ids == 0) return ok();
+    if (!ids || !dst || !aligned16(w) || !aligned16(dst))
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
+    if (!rxq4::device_info().arch_ok)
+        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+    return from_hip(rxq4::launch_embed(static_cast<uint16_t *>(dst),
+                                       static_cast<const uint8_t *>(w), ids, 0, n_vocab, n_ids,
+                                       hidden_dim, static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int rxq4_quantize_q4k(void *dst, const float *src, int64_t n_rows, int K, void *stream) {
+    const char *fn = "rxq4_quantize_q4k";
+    if (K <= 0 || K % 256 != 0 || n_rows < 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: K=%d n_rows=%lld", fn, K,
+                    (long long)n_rows);
+    if (n_rows == 0) return ok();
+    if (!dst || !src || !aligned16(dst) || !aligned16(src))
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
+    if (!rxq4::device_info().arch_ok)
+        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+    return from_hip(rxq4::launch_quantize(static_cast<uint8_t *>(dst), src, n_rows * (K / 256),
+                                          static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+const void *rxq4_resolve_weights(const void *w, const void *w_device) {
+    if (w_device) return w_device;
+    if (!w) return nullptr;
+    hipPointerAttribute_t attr;
+    memset(&attr, 0, sizeof(attr));
+    if (hipPointerGetAttributes(&attr, w) != hipSuccess) {
+        (void)hipGetLastError();  // ordinary host pointers report an error here
+        return nullptr;
+    }
+    if (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) return w;
+    return nullptr;
+}
+
+const char *rxq4_version(void) { return "rxq4 0.1.0 gfx950"; }
+
+const char *rxq4_last_error(void) { return g_last_error; }
+
+}  // extern "C"

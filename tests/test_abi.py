@@ -1,0 +1,73 @@
+"""The drop-in boundary, checked on the CPU (no GPU calls):
+  * include/reflex/infer.h has the reference header's binary layout (the same
+    probe compiled against both headers prints identical sizes, offsets,
+    enum values and constants);
+  * the library defines every public symbol the reference's dispatcher
+    defines and every kernel-seam symbol it needs
+    (reference src/dispatch.cpp, src/kernels/kernel_entrypoints.h:7-16);
+  * the library exports every entry point declared in include/rxq4.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE = os.path.join(ROOT, "oracle")
+LIB = os.path.join(ROOT, "reflex-infer_amd", "lib", "libreflex_infer_hip.so")
+REF = "/root/reference"
+HAVE_REF = os.path.exists(os.path.join(REF, "include", "reflex", "infer.h"))
+
+
+def _make(target):
+    subprocess.run(["make", "-s", "-C", ORACLE, target], check=True)
+
+
+def _probe(path):
+    return json.loads(subprocess.run([path], check=True, capture_output=True, text=True).stdout)
+
+
+@pytest.mark.skipif(not HAVE_REF, reason="reference checkout not present")
+def test_header_layout_matches_reference():
+    _make("_build/abi_probe_ours")
+    _make("_ref/abi_probe_ref")
+    ours = _probe(os.path.join(ORACLE, "_build", "abi_probe_ours"))
+    ref = _probe(os.path.join(ORACLE, "_ref", "abi_probe_ref"))
+    assert ours == ref
+    assert ours["GemvQuantArgs.sizeof"] == 56 and ours["GemvQuantTripleArgs.sizeof"] == 120
+
+
+def _nm(path, *flags):
+    out = subprocess.run(["nm", *flags, path], check=True, capture_output=True, text=True).stdout
+    syms = {}
+    for line in out.splitlines():
+        parts = line.split()
+        if len(parts) >= 2:
+            syms[parts[-1]] = parts[-2]
+    return syms
+
+
+@pytest.mark.skipif(not HAVE_REF, reason="reference checkout not present")
+def test_library_satisfies_reference_dispatcher_symbols():
+    _make("_ref/dispatch.o")
+    ref = _nm(os.path.join(ORACLE, "_ref", "dispatch.o"))
+    ours = _nm(LIB, "-D", "--defined-only")
+    defined = {s for s, t in ref.items() if t == "T"}
+    needed = {s for s, t in ref.items() if t == "U" and "reflex5infer7kernels" in s}
+    assert len(defined) == 11 and len(needed) == 9
+    assert defined <= set(ours), defined - set(ours)
+    assert needed <= set(ours), needed - set(ours)
+
+
+def test_library_exports_every_c_abi_entry_point():
+    header = open(os.path.join(ROOT, "include", "rxq4.h")).read()
+    names = set(re.findall(r"\b(rxq4_[a-z0-9_]+)\s*\(", header))
+    assert len(names) >= 12
+    lib = ctypes.CDLL(LIB)
+    for n in sorted(names):
+        assert hasattr(lib, n), n

@@ -1,0 +1,309 @@
+"""GPU parity of the HIP kernels against the CPU oracle and the golden fixtures.
+
+Bars (tests/util.py): dequantised weights and embedding rows bit-exact;
+GEMV/GEMM outputs within rel_err <= 1e-3 of the fp32/fp64 oracle over the
+same rounded operands, 16-bit outputs within 1 ulp of RNE(oracle).  Calls go
+through the C ABI (rxq4.capi) and the reflex::infer C++ API (rxq4.api).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import rxq4
+from oracle import oracle as orc
+from rxq4 import api, capi
+from tests import util
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "q4k_golden.npz")
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host16(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint16)
+
+
+def f16(bits: np.ndarray) -> np.ndarray:
+    return bits.view(np.float16).astype(np.float32)
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+# ------------------------------------------------------------ dequantisation
+def test_embedding_row_golden_bit_exact(golden):
+    table = dev(golden["emb_W"])
+    ids, expect = golden["emb_ids"], golden["emb_rows_f16"]
+    out = torch.empty(2048, dtype=torch.float16, device="cuda")
+    for i, t in enumerate(ids):
+        if not 0 <= t < 64:
+            continue
+        out.zero_()
+        a = api.DequantEmbeddingRowArgs(dst=out.data_ptr(), weights=table.data_ptr(),
+                                        ggml_type=12, token_id=int(t), hidden_dim=2048)
+        assert api.call("dequant_embedding_row", a) == rxq4.SUCCESS
+        assert np.array_equal(host16(out), expect[i]), t
+        out.zero_()
+        capi.embed_row_f16(out, table, int(t), 2048)
+        assert np.array_equal(host16(out), expect[i]), t
+
+
+def test_embedding_rows_batched_golden_and_oob(golden):
+    table = dev(golden["emb_W"])
+    ids = dev(golden["emb_ids"])
+    out = torch.full((ids.numel(), 2048), 7.0, dtype=torch.float16, device="cuda")
+    capi.embed_rows_f16(out, table, 64, ids, 2048)
+    assert np.array_equal(host16(out), golden["emb_rows_f16"])
+
+
+@pytest.mark.parametrize("K", [256, 2048, 11008])
+def test_embedding_rows_zipf(K):
+    vocab = 3000
+    Wn = util.weights(40 + K, vocab, K)
+    ids = util.zipf_ids(41, 4096, vocab)
+    W, idt = dev(Wn), dev(ids)
+    out = torch.empty((ids.size, K), dtype=torch.float16, device="cuda")
+    capi.embed_rows_f16(out, W, vocab, idt, K)
+    assert np.array_equal(host16(out), orc.embed_rows_f16(Wn, K, ids))
+
+
+def test_embedding_special_values():
+    """Subnormal, negative and zero scales dequantise bit-exactly too."""
+    from tests.test_oracle import random_blocks
+    K = 2048
+    Wn = random_blocks(42, 50, K)
+    out = torch.empty((50, K), dtype=torch.float16, device="cuda")
+    ids = np.arange(50, dtype=np.int32)
+    capi.embed_rows_f16(out, dev(Wn), 50, dev(ids), K)
+    got, ref = host16(out), orc.embed_rows_f16(Wn, K, ids)
+    with np.errstate(invalid="ignore"):
+        same = (got == ref) | (np.isnan(got.view(np.float16)) & np.isnan(ref.view(np.float16)))
+    assert same.all()
+
+
+@pytest.mark.parametrize("rows,K", [(64, 2048), (3, 11008), (1, 256), (500, 512)])
+def test_gpu_quantizer_matches_oracle(rows, K):
+    src = util.gaussian(43 + rows, (rows, K), 0.02)
+    src[0, :7] = [0, -0.0, 1e-8, -1e-8, 0.5, -0.7, 3e-3]
+    got = capi.quantize(dev(src)).cpu().numpy()
+    assert np.array_equal(got, orc.quantize(src))
+
+
+# ---------------------------------------------------------------------- GEMV
+SHAPES = [(2048, 2048), (7, 256), (33, 512), (2560, 2048), (301, 4096), (64, 11008),
+          (50, 2816), (3, 65536), (129, 1024)]
+
+
+@pytest.mark.parametrize("M,K", SHAPES)
+def test_gemv_f32_and_f16(M, K):
+    Wn = util.weights(50 + M + K, M, K)
+    x16 = util.x_f16(51 + K, K)
+    ref = orc.gemv_f32(Wn, K, x16)
+    W, x = dev(Wn), dev(x16)
+    y32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    capi.gemv_f32(y32, W, x, M, K)
+    assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL
+    y16 = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_f16(y16, W, x, M, K)
+    assert util.rel_err(f16(host16(y16)), ref) <= util.TOL
+    assert util.f16_ulp_dist(host16(y16), orc.f32_to_fp16(ref)).max() <= util.ULPS_OUT
+
+
+def test_gemv_golden(golden):
+    for case in ("c0", "c1", "c2"):
+        rows, K = (int(v) for v in golden[f"{case}_shape"])
+        W, x = dev(golden[f"{case}_W"]), dev(golden[f"{case}_x16"])
+        ref = golden[f"{case}_y_f32"].view(np.float32)
+        y32 = torch.empty(rows, dtype=torch.float32, device="cuda")
+        capi.gemv_f32(y32, W, x, rows, K)
+        assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL
+        y16 = torch.empty(rows, dtype=torch.float16, device="cuda")
+        capi.gemv_f16(y16, W, x, rows, K)
+        assert util.f16_ulp_dist(host16(y16), golden[f"{case}_y_f16"]).max() <= util.ULPS_OUT
+
+
+@pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 11008), (37, 512)])
+def test_gemv_add_and_in_place(M, K):
+    Wn = util.weights(60 + K, M, K)
+    x16, res16 = util.x_f16(61, K), util.x_f16(62, M)
+    ref = orc.gemv_add_f16(Wn, K, x16, res16)
+    W, x, res = dev(Wn), dev(x16), dev(res16)
+    y = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_add_f16(y, W, x, res, M, K)
+    assert util.f16_ulp_dist(host16(y), ref).max() <= 2
+    # y aliases residual (reference q4_gemm.cu:774-777 reads then writes per row)
+    a = api.GemvQuantAddArgs(y=res.data_ptr(), weights=W.data_ptr(), ggml_type=12,
+                             x=x.data_ptr(), residual=res.data_ptr(), M=M, K=K)
+    assert api.call("gemv_quant_add", a) == rxq4.SUCCESS
+    assert np.array_equal(host16(res), host16(y))
+
+
+def test_api_pair_and_triple_match_single_gemvs():
+    K = 2048
+    x16 = util.x_f16(70, K)
+    x = dev(x16)
+    # gate+up pair (11008 + 11008) and an odd split that straddles a wave step
+    for M0, M1 in [(11008, 11008), (3, 5)]:
+        W0n, W1n = util.weights(71, M0, K), util.weights(72, M1, K)
+        W0, W1 = dev(W0n), dev(W1n)
+        y0 = torch.empty(M0, dtype=torch.float16, device="cuda")
+        y1 = torch.empty(M1, dtype=torch.float16, device="cuda")
+        a = api.GemvQuantPairArgs(y0=y0.data_ptr(), weights0=W0.data_ptr(), ggml_type0=12, M0=M0,
+                                  y1=y1.data_ptr(), weights1=W1.data_ptr(), ggml_type1=12, M1=M1,
+                                  x=x.data_ptr(), K=K)
+        assert api.call("gemv_quant_pair", a) == rxq4.SUCCESS
+        for yv, Wn in ((y0, W0n), (y1, W1n)):
+            ref = orc.gemv_f32(Wn, K, x16)
+            assert util.f16_ulp_dist(host16(yv), orc.f32_to_fp16(ref)).max() <= 1
+    # fused QKV triple: 2048 / 256 / 256
+    Ms = (2048, 256, 256)
+    Wn = [util.weights(73 + i, m, K) for i, m in enumerate(Ms)]
+    Wd = [dev(w) for w in Wn]
+    ys = [torch.empty(m, dtype=torch.float16, device="cuda") for m in Ms]
+    a = api.GemvQuantTripleArgs(
+        y0=ys[0].data_ptr(), weights0=Wd[0].data_ptr(), ggml_type0=12, M0=Ms[0],
+        y1=ys[1].data_ptr(), weights1=Wd[1].data_ptr(), ggml_type1=12, M1=Ms[1],
+        y2=ys[2].data_ptr(), weights2=Wd[2].data_ptr(), ggml_type2=12, M2=Ms[2],
+        x=x.data_ptr(), K=K)
+    assert api.call("gemv_quant_triple", a) == rxq4.SUCCESS
+    for yv, w in zip(ys, Wn):
+        ref = orc.gemv_f32(w, K, x16)
+        assert util.f16_ulp_dist(host16(yv), orc.f32_to_fp16(ref)).max() <= 1
+
+
+def test_api_gemv_pointer_resolution():
+    """weights_device alias wins over a host `weights` pointer; a device
+    `weights` pointer resolves by itself; host memory alone is rejected."""
+    M, K = 256, 2048
+    Wn = util.weights(80, M, K)
+    x16 = util.x_f16(81, K)
+    ref16 = orc.f32_to_fp16(orc.gemv_f32(Wn, K, x16))
+    W, x = dev(Wn), dev(x16)
+    y = torch.empty(M, dtype=torch.float16, device="cuda")
+    host_ptr = Wn.ctypes.data
+    a = api.GemvQuantArgs(y=y.data_ptr(), weights=host_ptr, weights_device=W.data_ptr(),
+                          ggml_type=12, x=x.data_ptr(), M=M, K=K)
+    assert api.call("gemv_quant", a) == rxq4.SUCCESS
+    assert util.f16_ulp_dist(host16(y), ref16).max() <= 1
+    y.zero_()
+    a = api.GemvQuantArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=12, x=x.data_ptr(),
+                          M=M, K=K)
+    assert api.call("gemv_quant", a) == rxq4.SUCCESS
+    assert util.f16_ulp_dist(host16(y), ref16).max() <= 1
+    a = api.GemvQuantArgs(y=y.data_ptr(), weights=host_ptr, ggml_type=12, x=x.data_ptr(),
+                          M=M, K=K)
+    assert api.call("gemv_quant", a) == rxq4.INVALID_ARGUMENT
+    a = api.GemvQuantArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=14, x=x.data_ptr(),
+                          M=M, K=K)
+    assert api.call("gemv_quant", a) == rxq4.UNSUPPORTED_QUANT_FORMAT
+    f = api.GemvQuantF32Args(y=torch.empty(M, device="cuda").data_ptr(), weights=W.data_ptr(),
+                             ggml_type=12, x=x.data_ptr(), M=M, K=K)
+    assert api.call("gemv_quant_f32", f) == rxq4.SUCCESS
+
+
+def test_lm_head_full_size_properties():
+    """[151936 x 2048] fp32 logits: sampled rows vs the oracle; y(2x) == 2 y(x)
+    bit for bit (power-of-two scaling is exact); rows are independent (a row
+    permutation of W permutes y bit for bit)."""
+    M, K = 151936, 2048
+    g = torch.Generator(device="cuda").manual_seed(90)
+    src = torch.randn((M, K), generator=g, device="cuda") * 0.02
+    W = capi.quantize(src)
+    del src
+    x16 = util.x_f16(91, K)
+    x = dev(x16)
+    y = torch.empty(M, dtype=torch.float32, device="cuda")
+    capi.gemv_f32(y, W, x, M, K)
+    rows = np.sort(util.rng(92).choice(M, 1024, replace=False))
+    Wn = W[torch.from_numpy(rows).cuda()].cpu().numpy()
+    ref = orc.gemv_f32(Wn, K, x16)
+    assert util.rel_err(y.cpu().numpy()[rows], ref) <= util.TOL
+    x2 = (x.view(torch.float16) * 2).view(torch.int16)
+    y2 = torch.empty_like(y)
+    capi.gemv_f32(y2, W, x2, M, K)
+    assert torch.equal(y2, y * 2)
+    perm = torch.randperm(M, generator=torch.Generator().manual_seed(93)).cuda()
+    Wp = W[perm].contiguous()
+    yp = torch.empty_like(y)
+    capi.gemv_f32(yp, Wp, x, M, K)
+    assert torch.equal(yp, y[perm])
+
+
+# ---------------------------------------------------------------------- GEMM
+GEMM_CASES = [(300, 2, 2048), (2048, 5, 2048), (1000, 16, 2048), (2048, 17, 2048),
+              (300, 100, 11008), (2048, 512, 2048), (129, 33, 512)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_CASES)
+def test_gemm_bf16(M, N, K):
+    Wn = util.weights(100 + M + N, M, K)
+    xb = util.f32_to_bf16_bits(util.gaussian(101 + N, (N, K)))
+    xv = orc.bits_bf16_to_f32(xb)
+    ref = orc.gemm_f64(Wn, K, xv, "bf16")
+    W = dev(Wn)
+    x = torch.from_numpy(xb.view(np.int16)).cuda().view(torch.bfloat16)
+    y32 = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    capi.gemm(y32, W, x, M, N, K)
+    assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL
+    yb = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+    capi.gemm(yb, W, x, M, N, K)
+    got = yb.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert util.bf16_ulp_dist(got, util.f32_to_bf16_bits(ref.astype(np.float32))).max() <= util.ULPS_OUT
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 3, 2048), (2048, 16, 2048), (1000, 40, 2048),
+                                   (256, 512, 2048), (200, 20, 11008)])
+def test_api_gemm_quant_batched_f16(M, N, K):
+    Wn = util.weights(110 + N, M, K)
+    x16 = util.x_f16(111 + N, (N, K))
+    ref32 = orc.gemm_tokens_f32(Wn, K, x16)   # reference CPU semantics (per-token GEMV)
+    ref64 = orc.gemm_f64(Wn, K, f16(x16), "f16")  # same operands as the fp16 MFMA tiles
+    W, x = dev(Wn), dev(x16)
+    y = torch.empty((N, M), dtype=torch.float16, device="cuda")
+    a = api.GemmQuantBatchedArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=12,
+                                 x=x.data_ptr(), M=M, N=N, K=K)
+    assert api.call("gemm_quant_batched", a) == rxq4.SUCCESS
+    got = f16(host16(y))
+    assert util.rel_err(got, ref32) <= util.TOL
+    assert util.f16_ulp_dist(host16(y), orc.f32_to_fp16(ref64.astype(np.float32))).max() <= 1
+
+
+def test_gemm_n1_is_the_gemv():
+    M, K = 512, 2048
+    Wn = util.weights(120, M, K)
+    x16 = util.x_f16(121, (1, K))
+    W, x = dev(Wn), dev(x16)
+    y = torch.empty((1, M), dtype=torch.float16, device="cuda")
+    capi.gemm_f16(y, W, x, M, 1, K)
+    y2 = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_f16(y2, W, x, M, K)
+    assert torch.equal(y[0], y2)
+
+
+def test_gemm_full_size_sampled_rows():
+    """m = 512 tokens on [11008 x 2048]: 256 sampled rows vs the fp64 oracle."""
+    M, N, K = 11008, 512, 2048
+    g = torch.Generator(device="cuda").manual_seed(130)
+    W = capi.quantize(torch.randn((M, K), generator=g, device="cuda") * 0.02)
+    x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    capi.gemm(y, W, x, M, N, K)
+    rows = np.sort(util.rng(131).choice(M, 256, replace=False))
+    Wn = W[torch.from_numpy(rows).cuda()].cpu().numpy()
+    xv = x.float().cpu().numpy()
+    ref = orc.gemm_f64(Wn, K, xv, "bf16")
+    assert util.rel_err(y.cpu().numpy()[:, rows], ref) <= util.TOL
