@@ -15,8 +15,10 @@
 //   * per slot: y += d*sc_lo*S_lo - dmin*m_lo*sum_lo + (d*sc_hi/16)*S_hi -
 //     dmin*m_hi*sum_hi, i.e. the reference's w = d*sc*q - dmin*m factored
 //     over the sub-block;
-//   * rows are reduced across their lanes with cross-lane adds.
-// Work: ~1.5 VALU ops per weight, under the ~2.8 ops/weight that 8 TB/s of
+//   * the lanes of a row are summed with DPP row rotations and broadcasts;
+//   * loads for the next batch of rows are issued before the current batch is
+//     computed (two register buffers), so memory and VALU overlap per wave.
+// Work: ~1.6 VALU ops per weight, under the ~2.8 ops/weight that 8 TB/s of
 // 4.5-bit weights leaves on 256 CUs.  Bytes per launch: rows*K/256*144 +
 // K*2 + rows*out_bytes (+ rows*2 residual).
 #include "launch.h"
@@ -75,197 +77,304 @@ __device__ __forceinline__ void load_x_slot(const uint16_t *__restrict__ x, int 
     s.bias_hi = -1024.0f * sh;
 }
 
+// Lane-constant parts of the scale decode for quant group il.  With
+// s0/s1/s2 the scale dwords (bytes 0-3, 4-7, 8-11 of the 12 scale bytes) and
+// h = 16*(il & 1):
+//   il < 2:  sc = (s0 >> h) & 0x3F3F,  m = (s1 >> h) & 0x3F3F
+//   il >= 2: sc = (s2 >> h) & 0x0F0F | (s0 >> (h+2)) & 0x3030,
+//            m  = (s2 >> (h+4)) & 0x0F0F | (s1 >> (h+2)) & 0x3030
+// i.e. sc = (s0 >> shA) & mA | (s2 >> h) & mC, m = (s1 >> shA) & mA |
+// (s2 >> (h+4)) & mC with the constants below; byte 0 / byte 1 of sc, m are
+// the pairs of sub-blocks 2*il and 2*il+1 (get_scale_min_k4, q4_gemm.cu:192-202).
+struct ScaleDecode {
+    uint32_t shA, shC, shC4, mA, mC;
+};
+
+__device__ __forceinline__ ScaleDecode scale_decode_for(int il) {
+    const uint32_t h = (uint32_t)(il & 1) << 4;
+    const bool upper = il >= 2;
+    return ScaleDecode{h + (upper ? 2u : 0u), h, h + 4u, upper ? 0x3030u : 0x3F3Fu,
+                       upper ? 0x0F0Fu : 0u};
+}
+
+// v_and_or_b32 with the mask in an SGPR and the magic in a VGPR (a VOP3 may
+// read one scalar operand, so the compiler cannot fuse two literal constants).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(magic));
+    return r;
+}
+
 // Partial dot product of one slot of one row.
 __device__ __forceinline__ float slot_dot(u32x4 hdr, u32x4 q0, u32x4 q1, const XSlot &s,
-                                          int il) {
+                                          const ScaleDecode &sd, uint32_t magic) {
     const float d = f16_bits_to_f32(hdr.x & 0xFFFFu);
     const float dmin = f16_bits_to_f32(hdr.x >> 16);
-    uint32_t sc, mn;
-    scale_pair(hdr.y, hdr.z, hdr.w, il, &sc, &mn);
+    const uint32_t sc = ((hdr.y >> sd.shA) & sd.mA) | ((hdr.w >> sd.shC) & sd.mC);
+    const uint32_t mn = ((hdr.z >> sd.shA) & sd.mA) | ((hdr.w >> sd.shC4) & sd.mC);
     const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     float acc_lo = s.bias_lo, acc_hi = s.bias_hi;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const uint32_t v = q[k], v8 = q[k] >> 8;
-        acc_lo = __builtin_amdgcn_fdot2(as_half2((v & 0x000F000Fu) | 0x64006400u),
+        acc_lo = __builtin_amdgcn_fdot2(as_half2(and_or(v, 0x000F000Fu, magic)),
                                         as_half2(s.p[4 * k + 0]), acc_lo, false);
-        acc_lo = __builtin_amdgcn_fdot2(as_half2((v8 & 0x000F000Fu) | 0x64006400u),
+        acc_lo = __builtin_amdgcn_fdot2(as_half2(and_or(v8, 0x000F000Fu, magic)),
                                         as_half2(s.p[4 * k + 1]), acc_lo, false);
-        acc_hi = __builtin_amdgcn_fdot2(as_half2((v & 0x00F000F0u) | 0x64006400u),
+        acc_hi = __builtin_amdgcn_fdot2(as_half2(and_or(v, 0x00F000F0u, magic)),
                                         as_half2(s.p[4 * k + 2]), acc_hi, false);
-        acc_hi = __builtin_amdgcn_fdot2(as_half2((v8 & 0x00F000F0u) | 0x64006400u),
+        acc_hi = __builtin_amdgcn_fdot2(as_half2(and_or(v8, 0x00F000F0u, magic)),
                                         as_half2(s.p[4 * k + 3]), acc_hi, false);
     }
     const float d_lo = d * (float)(sc & 0xFFu);
-    const float d_hi = d * (float)(sc >> 8) * 0.0625f;
+    const float d_hi = (d * 0.0625f) * (float)((sc >> 8) & 0xFFu);
     const float m_lo = dmin * (float)(mn & 0xFFu);
-    const float m_hi = dmin * (float)(mn >> 8);
+    const float m_hi = dmin * (float)((mn >> 8) & 0xFFu);
     return d_lo * acc_lo - m_lo * s.sx_lo + (d_hi * acc_hi - m_hi * s.sx_hi);
 }
 
-// The (up to three) output ranges as plain values.  Kernels copy them out of
-// the parameter block field by field so that selecting a range is a register
-// select, never an indexed load from a stack copy of the parameters.
-struct Ranges {
-    const uint8_t *w0, *w1, *w2;
-    void *y0, *y1, *y2;
-    const uint16_t *r0, *r1, *r2;
-    int m0, m1, n;
+// DPP control words (GFX9): row_ror:n = 0x120 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                  0xF, false);
+    return v + __builtin_bit_cast(float, moved);
+}
+
+// Sum over aligned groups of W lanes (W in {4, 8, 16, 32, 64}).  The full sum
+// is valid in lane W-1 of every group (and in every lane of the group for
+// W <= 16).
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    if (W >= 16) {
+        v = dpp_add<0x128, 0xF>(v);  // row_ror:8
+        v = dpp_add<0x124, 0xF>(v);  // row_ror:4
+        v = dpp_add<0x122, 0xF>(v);  // row_ror:2
+        v = dpp_add<0x121, 0xF>(v);  // row_ror:1
+        if (W >= 32) v = dpp_add<0x142, 0xA>(v);  // rows 1, 3 += last lane of rows 0, 2
+        if (W >= 64) v = dpp_add<0x143, 0xC>(v);  // rows 2, 3 += lane 31
+    } else {
+#pragma unroll
+        for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    }
+    return v;
+}
+
+// One output range, copied out of the kernel parameter block field by field
+// so that picking a range is a scalar select, never an indexed load from a
+// stack copy of the parameters.
+struct Range {
+    const uint8_t *w;
+    void *y;
+    const uint16_t *res;
+    int rows;
+    int first_unit;
 };
 
-__device__ __forceinline__ Ranges ranges_of(const GemvParams &p) {
-    return Ranges{p.r[0].w, p.r[1].w, p.r[2].w, p.r[0].y, p.r[1].y, p.r[2].y,
-                  p.r[0].res, p.r[1].res, p.r[2].res, p.r[0].rows, p.r[1].rows, p.n_ranges};
-}
-
-// Row -> (range, local row).  Ranges are concatenated in order.
-__device__ __forceinline__ int locate(const Ranges &g, int row, int *local) {
-    int ri = 0;
-    if (g.n > 1 && row >= g.m0) {
-        row -= g.m0;
-        ri = 1;
-        if (g.n > 2 && row >= g.m1) {
-            row -= g.m1;
-            ri = 2;
-        }
-    }
-    *local = row;
-    return ri;
-}
-
-__device__ __forceinline__ const uint8_t *range_w(const Ranges &g, int ri) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(g.w0), b = reinterpret_cast<uintptr_t>(g.w1),
-                    c = reinterpret_cast<uintptr_t>(g.w2);
-    return reinterpret_cast<const uint8_t *>(ri == 0 ? a : (ri == 1 ? b : c));
+__device__ __forceinline__ Range range_of_unit(const GemvParams &p, int unit) {
+    const uint8_t *w0 = p.r[0].w, *w1 = p.r[1].w, *w2 = p.r[2].w;
+    void *y0 = p.r[0].y, *y1 = p.r[1].y, *y2 = p.r[2].y;
+    const uint16_t *r0 = p.r[0].res, *r1 = p.r[1].res, *r2 = p.r[2].res;
+    const int m0 = p.r[0].rows, m1 = p.r[1].rows, m2 = p.r[2].rows;
+    const int u1 = p.unit_start[1], u2 = p.unit_start[2];
+    const int ri = (p.n_ranges > 1 && unit >= u1) ? ((p.n_ranges > 2 && unit >= u2) ? 2 : 1) : 0;
+    Range r;
+    r.w = ri == 0 ? w0 : (ri == 1 ? w1 : w2);
+    r.y = ri == 0 ? y0 : (ri == 1 ? y1 : y2);
+    r.res = ri == 0 ? r0 : (ri == 1 ? r1 : r2);
+    r.rows = ri == 0 ? m0 : (ri == 1 ? m1 : m2);
+    r.first_unit = ri == 0 ? 0 : (ri == 1 ? u1 : u2);
+    return r;
 }
 
 template <int EPI>
-__device__ __forceinline__ void store_row(const Ranges &g, int ri, int local, float v) {
-    const uintptr_t ya = reinterpret_cast<uintptr_t>(g.y0), yb = reinterpret_cast<uintptr_t>(g.y1),
-                    yc = reinterpret_cast<uintptr_t>(g.y2);
-    void *y = reinterpret_cast<void *>(ri == 0 ? ya : (ri == 1 ? yb : yc));
+__device__ __forceinline__ void store_row(const Range &r, int row, float v) {
     if (EPI == kEpiF32) {
-        static_cast<float *>(y)[local] = v;
+        static_cast<float *>(r.y)[row] = v;
     } else if (EPI == kEpiF16) {
-        static_cast<uint16_t *>(y)[local] = f32_to_f16_bits(v);
+        static_cast<uint16_t *>(r.y)[row] = f32_to_f16_bits(v);
     } else {
-        const uintptr_t ra = reinterpret_cast<uintptr_t>(g.r0), rb = reinterpret_cast<uintptr_t>(g.r1),
-                        rc = reinterpret_cast<uintptr_t>(g.r2);
-        const uint16_t *res = reinterpret_cast<const uint16_t *>(ri == 0 ? ra : (ri == 1 ? rb : rc));
+        // q4_gemm.cu:774-777: round the projection, add the residual, round.
         const float projected = f16_bits_to_f32(f32_to_f16_bits(v));
-        static_cast<uint16_t *>(y)[local] =
-            f32_to_f16_bits(projected + f16_bits_to_f32(res[local]));
+        static_cast<uint16_t *>(r.y)[row] =
+            f32_to_f16_bits(projected + f16_bits_to_f32(r.res[row]));
     }
 }
 
-// Register kernel: a row has LPR = 4*nb <= 64 slots (nb in {1,2,4,8,16}), so
-// a wave covers 64/LPR rows per step and each lane's slot never changes.
-// Wave w owns rows [w*rows_per_unit, (w+1)*rows_per_unit); U steps of loads
-// are issued before any arithmetic.
+__device__ __forceinline__ uint32_t magic_vgpr() {
+    uint32_t m;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(m));
+    return m;
+}
+
+template <int U>
+struct Batch {
+    u32x4 h[U], a[U], c[U];
+};
+
+// ---------------------------------------------------------------------------
+// Register kernel: a row has LPR = 4*nb <= 64 slots (nb in {1,2,4,8,16}), so a
+// wave covers RPS = 64/LPR rows per step and each lane's slot never changes.
+// Wave w serves steps [t0, t1) of one range; batches of U steps are loaded one
+// batch ahead of the arithmetic.
 template <int LPR, int EPI, int U>
 __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
     constexpr int RPS = 64 / LPR;
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int row_begin = wave * p.rows_per_unit;
-    if (row_begin >= p.total_rows) return;
-    const int row_end = min(row_begin + p.rows_per_unit, p.total_rows);
+    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (wave >= p.total_units) return;
+    const Range rg = range_of_unit(p, wave);
+    const int n_steps = (rg.rows + RPS - 1) / RPS;
+    const int t0 = (wave - rg.first_unit) * p.per_unit;
+    const int t1 = min(t0 + p.per_unit, n_steps);
+    if (t0 >= t1) return;
+
     const int slot = lane & (LPR - 1);
     const int sub = lane / LPR;
     const int b = slot >> 2, il = slot & 3;
-    const Ranges rg = ranges_of(p);
+    const uint32_t row_bytes = (uint32_t)p.nb * kBlockBytes;
+    const uint32_t hdr_off = (uint32_t)b * kBlockBytes;
+    const uint32_t q_off = hdr_off + 16u + 32u * (uint32_t)il;
+    const int last = rg.rows - 1;
 
+    auto load = [&](int t, Batch<U> &bt) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int ts = min(t + u, t1 - 1);
+            // uniform part: first row of the step; lane part: sub-row, clamped
+            const uint8_t *base = rg.w + (int64_t)(ts * RPS) * row_bytes;
+            const uint32_t lrow = (uint32_t)min(sub, last - ts * RPS) * row_bytes;
+            bt.h[u] = load16(base + (lrow + hdr_off));
+            bt.a[u] = load16(base + (lrow + q_off));
+            bt.c[u] = load16(base + (lrow + q_off + 16u));
+        }
+    };
+    // First weight batch goes out before the activations, so the two memory
+    // round trips overlap.
+    Batch<U> A, B;
+    load(t0, A);
     XSlot xs;
     load_x_slot(p.x, b, il, true, xs);
-    const int64_t row_bytes = (int64_t)p.nb * kBlockBytes;
-    const int slot_off = b * kBlockBytes;
+    const ScaleDecode sd = scale_decode_for(il);
+    const uint32_t magic = magic_vgpr();
+    auto compute = [&](int t, const Batch<U> &bt) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float v = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic);
+            v = lane_group_sum<LPR>(v);
+            const int row = (t + u) * RPS + sub;
+            if (slot == LPR - 1 && t + u < t1 && row < rg.rows) store_row<EPI>(rg, row, v);
+        }
+    };
 
-    for (int r0 = row_begin; r0 < row_end; r0 += RPS * U) {
-        u32x4 h[U], a[U], c[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int row = min(r0 + u * RPS + sub, row_end - 1);
-            int local;
-            const int ri = locate(rg, row, &local);
-            const uint8_t *blk = range_w(rg, ri) + local * row_bytes + slot_off;
-            h[u] = load16(blk);
-            a[u] = load16(blk + 16 + 32 * il);
-            c[u] = load16(blk + 32 + 32 * il);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float v = slot_dot(h[u], a[u], c[u], xs, il);
-            v = group_sum<LPR>(v);
-            const int row = r0 + u * RPS + sub;
-            if (slot == 0 && row < row_end) {
-                int local;
-                const int ri = locate(rg, row, &local);
-                store_row<EPI>(rg, ri, local, v);
-            }
-        }
+    for (int t = t0; t < t1; t += 2 * U) {
+        if (t + U < t1) load(t + U, B);
+        compute(t, A);
+        if (t + U >= t1) break;
+        if (t + 2 * U < t1) load(t + 2 * U, A);
+        compute(t + U, B);
     }
 }
 
-// Split kernel for rows with more than 64 slots: a workgroup of J waves covers
-// one row, wave j holding slots [64j, 64j+64) in registers; per row the J
-// wave sums meet in LDS and are added in wave order.  Workgroup g owns rows
-// [g*rows_per_unit, (g+1)*rows_per_unit), U rows per round.
-constexpr int kMaxSplitWaves = 16;
+// ---------------------------------------------------------------------------
+// LDS kernel for rows with more than 64 slots (any K): the workgroup stages
+// x once in LDS in the same permuted-pair layout (36 dwords per slot), and
+// each wave owns whole rows, walking a row's slots 64 at a time
+// (J = ceil(4*nb/64) items per row).  Items (row, j) are processed U at a
+// time with the next batch of weights in flight; the row's lanes are summed
+// once per row.  No barrier after the staging barrier.
+constexpr int kLdsSlotWords = 36;
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 template <int EPI, int U>
-__global__ __launch_bounds__(1024) void gemv_split_kernel(GemvParams p) {
-    __shared__ float part[2][kMaxSplitWaves][U];
+__global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
+    extern __shared__ uint32_t xlds[];
     const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const int n_waves = blockDim.x >> 6;
-    const int slot = wv * 64 + lane;
-    const bool valid = slot < 4 * p.nb;
-    const int b = slot >> 2, il = slot & 3;
-    const int row_begin = blockIdx.x * p.rows_per_unit;
-    const int row_end = min(row_begin + p.rows_per_unit, p.total_rows);
-    const Ranges rg = ranges_of(p);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_slots = 4 * p.nb;
+    const int J = (n_slots + 63) >> 6;
+    const int wave = blockIdx.x * 4 + wv;
+    const bool active = wave < p.total_units;
+    const Range rg = range_of_unit(p, active ? wave : 0);
+    const int r0 = (wave - rg.first_unit) * p.per_unit;
+    const int r1 = active ? min(r0 + p.per_unit, rg.rows) : r0;
+    const int n_items = (r1 > r0 ? r1 - r0 : 0) * J;
+    const uint32_t row_bytes = (uint32_t)p.nb * kBlockBytes;
 
-    XSlot xs;
-    load_x_slot(p.x, b, il, valid, xs);
-    const int64_t row_bytes = (int64_t)p.nb * kBlockBytes;
-    const int slot_off = b * kBlockBytes;
-
-    int buf = 0;
-    for (int r0 = row_begin; r0 < row_end; r0 += U, buf ^= 1) {
-        u32x4 h[U], a[U], c[U];
+    // Items are walked in order by two cursors (loads run one batch ahead of
+    // the arithmetic): item (row, j) covers slots [64j, 64j+64) of the row.
+    int ld_row = r0, ld_j = 0;
+    auto load = [&](Batch<U> &bt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (valid) {
-                const int row = min(r0 + u, row_end - 1);
-                int local;
-                const int ri = locate(rg, row, &local);
-                const uint8_t *blk = range_w(rg, ri) + local * row_bytes + slot_off;
-                h[u] = load16(blk);
-                a[u] = load16(blk + 16 + 32 * il);
-                c[u] = load16(blk + 32 + 32 * il);
-            } else {
-                h[u] = u32x4{0, 0, 0, 0};
-                a[u] = h[u];
-                c[u] = h[u];
-            }
+            const int row = min(ld_row, r1 - 1);
+            const int slot = min(64 * ld_j + lane, n_slots - 1);
+            const uint8_t *blk = rg.w + (int64_t)row * row_bytes + (slot >> 2) * kBlockBytes;
+            bt.h[u] = load16(blk);
+            bt.a[u] = load16(blk + 16 + 32 * (slot & 3));
+            bt.c[u] = load16(blk + 32 + 32 * (slot & 3));
+            if (++ld_j == J) { ld_j = 0; ++ld_row; }
         }
+    };
+    Batch<U> A, B;
+    if (n_items > 0) load(A);
+
+    // Stage x: one slot per thread and round.
+    for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
+        XSlot xs;
+        load_x_slot(p.x, s >> 2, s & 3, true, xs);
+        uint32_t *dst = xlds + s * kLdsSlotWords;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            *reinterpret_cast<u32x4 *>(dst + 4 * k) =
+                u32x4{xs.p[4 * k], xs.p[4 * k + 1], xs.p[4 * k + 2], xs.p[4 * k + 3]};
+        *reinterpret_cast<f32x4v *>(dst + 32) = f32x4v{xs.bias_lo, xs.bias_hi, xs.sx_lo, xs.sx_hi};
+    }
+    __syncthreads();
+    if (n_items == 0) return;
+
+    const uint32_t magic = magic_vgpr();
+    float acc = 0.0f;
+    int cp_row = r0, cp_j = 0;
+    auto compute = [&](const Batch<U> &bt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float v = valid ? slot_dot(h[u], a[u], c[u], xs, il) : 0.0f;
-            v = group_sum<64>(v);
-            if (lane == 0) part[buf][wv][u] = v;
-        }
-        __syncthreads();
-        if (wv == 0 && lane < U) {
-            const int row = r0 + lane;
-            if (row < row_end) {
-                float s = 0.0f;
-                for (int j = 0; j < n_waves; ++j) s += part[buf][j][lane];
-                int local;
-                const int ri = locate(rg, row, &local);
-                store_row<EPI>(rg, ri, local, s);
+            if (cp_row < r1) {  // uniform
+                const int slot = 64 * cp_j + lane;
+                const bool valid = slot < n_slots;
+                const int sl = valid ? slot : 0;
+                const uint32_t *src = xlds + sl * kLdsSlotWords;
+                XSlot xs;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(src + 4 * k);
+                    xs.p[4 * k] = v.x; xs.p[4 * k + 1] = v.y; xs.p[4 * k + 2] = v.z; xs.p[4 * k + 3] = v.w;
+                }
+                const f32x4v t = *reinterpret_cast<const f32x4v *>(src + 32);
+                xs.bias_lo = t[0];
+                xs.bias_hi = t[1];
+                xs.sx_lo = t[2];
+                xs.sx_hi = t[3];
+                const ScaleDecode sd = scale_decode_for(sl & 3);
+                const float v = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic);
+                acc += valid ? v : 0.0f;
+                if (++cp_j == J) {
+                    const float total = lane_group_sum<64>(acc);
+                    if (lane == 63) store_row<EPI>(rg, cp_row, total);
+                    acc = 0.0f;
+                    cp_j = 0;
+                    ++cp_row;
+                }
             }
         }
+    };
+    for (int i = 0; i < n_items; i += 2 * U) {
+        if (i + U < n_items) load(B);
+        compute(A);
+        if (i + U >= n_items) break;
+        if (i + 2 * U < n_items) load(A);
+        compute(B);
     }
 }
 
@@ -291,12 +400,29 @@ const DeviceInfo &device_info() {
 static int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     if (!v || !*v) return dflt;
-    return atoi(v);
+    const int r = atoi(v);
+    return r > 0 ? r : dflt;
+}
+
+// Cut each range into units of `per_unit` items (an item is `rows_per_item`
+// rows); returns the unit count.  Units never straddle two ranges.
+static int assign_units(GemvParams &p, int rows_per_item, int per_unit) {
+    int units = 0;
+    p.unit_start[0] = 0;
+    for (int i = 0; i < p.n_ranges; ++i) {
+        if (i > 0) p.unit_start[i] = units;
+        const int items = (p.r[i].rows + rows_per_item - 1) / rows_per_item;
+        units += (items + per_unit - 1) / per_unit;
+    }
+    for (int i = p.n_ranges; i < 3; ++i) p.unit_start[i] = units;
+    p.per_unit = per_unit;
+    p.total_units = units;
+    return units;
 }
 
 template <int LPR, int EPI>
 static void launch_reg(const GemvParams &p, int grid, hipStream_t st) {
-    gemv_reg_kernel<LPR, EPI, 4><<<grid, 256, 0, st>>>(p);
+    gemv_reg_kernel<LPR, EPI, 2><<<grid, 256, 0, st>>>(p);
 }
 
 template <int EPI>
@@ -304,16 +430,14 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
     const int slots = 4 * p.nb;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
     if (slots <= 64 && (64 % slots) == 0) {
-        // Register kernel.  Aim for `waves_per_cu` resident waves per CU.
+        // Register kernel: aim for `waves_per_cu` waves per CU over the launch.
         const int rps = 64 / slots;
-        const int waves_per_cu = env_int("RXQ4_GEMV_WAVES_PER_CU", 8);
         const int64_t steps = (p.total_rows + rps - 1) / rps;
-        const int64_t target = (int64_t)cus * (waves_per_cu > 0 ? waves_per_cu : 8);
-        int64_t steps_per_wave = (steps + target - 1) / target;
-        if (steps_per_wave < 1) steps_per_wave = 1;
-        p.rows_per_unit = (int)(steps_per_wave * rps);
-        const int64_t waves = (p.total_rows + p.rows_per_unit - 1) / p.rows_per_unit;
-        const int grid = (int)((waves + 3) / 4);
+        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_WAVES_PER_CU", 8);
+        int per_wave = (int)((steps + target - 1) / target);
+        if (per_wave < 1) per_wave = 1;
+        const int waves = assign_units(p, rps, per_wave);
+        const int grid = (waves + 3) / 4;
         switch (slots) {
             case 4: launch_reg<4, EPI>(p, grid, st); break;
             case 8: launch_reg<8, EPI>(p, grid, st); break;
@@ -322,16 +446,21 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
             default: launch_reg<64, EPI>(p, grid, st); break;
         }
     } else {
-        const int j = (slots + 63) / 64;
-        if (j > kMaxSplitWaves) return hipErrorInvalidValue;
-        constexpr int U = 4;
-        const int groups_per_cu = env_int("RXQ4_GEMV_GROUPS_PER_CU", 16 / j > 1 ? 16 / j : 1);
-        const int64_t target = (int64_t)cus * (groups_per_cu > 0 ? groups_per_cu : 1);
-        int64_t rounds = ((int64_t)p.total_rows + U * target - 1) / (U * target);
-        if (rounds < 1) rounds = 1;
-        p.rows_per_unit = (int)(rounds * U);
-        const int grid = (p.total_rows + p.rows_per_unit - 1) / p.rows_per_unit;
-        gemv_split_kernel<EPI, U><<<grid, 64 * j, 0, st>>>(p);
+        // LDS kernel: whole rows per wave, `waves_per_cu` waves per CU.
+        const size_t lds = (size_t)slots * kLdsSlotWords * sizeof(uint32_t);
+        if (lds > 160 * 1024) return hipErrorInvalidValue;
+        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_LDS_WAVES_PER_CU", 8);
+        int per_wave = (int)((p.total_rows + target - 1) / target);
+        if (per_wave < 1) per_wave = 1;
+        const int waves = assign_units(p, 1, per_wave);
+        const int grid = (waves + 3) / 4;
+        if (lds > 64 * 1024) {
+            const hipError_t e = hipFuncSetAttribute(
+                reinterpret_cast<const void *>(&gemv_lds_kernel<EPI, 2>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        gemv_lds_kernel<EPI, 2><<<grid, 256, lds, st>>>(p);
     }
     return hipGetLastError();
 }

@@ -17,13 +17,19 @@ struct GemvRange {
     int rows;
 };
 
+// Work is cut into "units" (a wave of the register kernel, a workgroup of the
+// split kernel); every unit belongs to exactly one range, so the range is
+// uniform across the unit.  Units [unit_start[i], unit_start[i+1]) serve
+// range i.
 struct GemvParams {
     GemvRange r[3];
     int n_ranges;
     int total_rows;
-    const uint16_t *x;  // fp16 [K], 16-byte aligned
-    int nb;             // Q4_K blocks per row = K / 256
-    int rows_per_unit;  // rows per wave (register kernel) or per workgroup (split kernel)
+    const uint16_t *x;   // fp16 [K], 16-byte aligned
+    int nb;              // Q4_K blocks per row = K / 256
+    int per_unit;        // steps per wave (register kernel) / rows per workgroup (split)
+    int unit_start[3];   // first unit of ranges 1..2 in [1], [2]; [0] = 0
+    int total_units;
 };
 
 struct DeviceInfo {

@@ -2,7 +2,8 @@
 
 Bars (tests/util.py): dequantised weights and embedding rows bit-exact;
 GEMV/GEMM outputs within rel_err <= 1e-3 of the fp32/fp64 oracle over the
-same rounded operands, 16-bit outputs within 1 ulp of RNE(oracle).  Calls go
+same rounded operands, 16-bit outputs correctly rounded up to accumulation
+order (tests/util.py rounded_ok).  Calls go
 through the C ABI (rxq4.capi) and the reflex::infer C++ API (rxq4.api).
 """
 from __future__ import annotations
@@ -120,7 +121,7 @@ def test_gemv_f32_and_f16(M, K):
     y16 = torch.empty(M, dtype=torch.float16, device="cuda")
     capi.gemv_f16(y16, W, x, M, K)
     assert util.rel_err(f16(host16(y16)), ref) <= util.TOL
-    assert util.f16_ulp_dist(host16(y16), orc.f32_to_fp16(ref)).max() <= util.ULPS_OUT
+    assert util.rounded_ok(host16(y16), ref).all()
 
 
 def test_gemv_golden(golden):
@@ -133,18 +134,25 @@ def test_gemv_golden(golden):
         assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL
         y16 = torch.empty(rows, dtype=torch.float16, device="cuda")
         capi.gemv_f16(y16, W, x, rows, K)
-        assert util.f16_ulp_dist(host16(y16), golden[f"{case}_y_f16"]).max() <= util.ULPS_OUT
+        assert util.rounded_ok(host16(y16), ref).all()
+        assert util.rel_err(f16(host16(y16)), f16(golden[f"{case}_y_f16"])) <= util.TOL
 
 
 @pytest.mark.parametrize("M,K", [(2048, 2048), (2048, 11008), (37, 512)])
 def test_gemv_add_and_in_place(M, K):
     Wn = util.weights(60 + K, M, K)
     x16, res16 = util.x_f16(61, K), util.x_f16(62, M)
-    ref = orc.gemv_add_f16(Wn, K, x16, res16)
+    ref16 = orc.gemv_add_f16(Wn, K, x16, res16)
+    y32 = orc.gemv_f32(Wn, K, x16)
     W, x, res = dev(Wn), dev(x16), dev(res16)
     y = torch.empty(M, dtype=torch.float16, device="cuda")
     capi.gemv_add_f16(y, W, x, res, M, K)
-    assert util.f16_ulp_dist(host16(y), ref).max() <= 2
+    # double rounding: the projection is rounded to fp16 before the add
+    # (q4_gemm.cu:774-777), which may move it by half an ulp of the projection
+    proj_sp = util.spacing(orc.f32_to_fp16(y32), "f16")
+    exact = y32.astype(np.float64) + f16(res16)
+    assert util.rounded_ok(host16(y), exact, delta=util.ACC_DELTA, extra=proj_sp / 2).all()
+    assert util.rel_err(f16(host16(y)), f16(ref16)) <= util.TOL
     # y aliases residual (reference q4_gemm.cu:774-777 reads then writes per row)
     a = api.GemvQuantAddArgs(y=res.data_ptr(), weights=W.data_ptr(), ggml_type=12,
                              x=x.data_ptr(), residual=res.data_ptr(), M=M, K=K)
@@ -168,7 +176,7 @@ def test_api_pair_and_triple_match_single_gemvs():
         assert api.call("gemv_quant_pair", a) == rxq4.SUCCESS
         for yv, Wn in ((y0, W0n), (y1, W1n)):
             ref = orc.gemv_f32(Wn, K, x16)
-            assert util.f16_ulp_dist(host16(yv), orc.f32_to_fp16(ref)).max() <= 1
+            assert util.rounded_ok(host16(yv), ref).all()
     # fused QKV triple: 2048 / 256 / 256
     Ms = (2048, 256, 256)
     Wn = [util.weights(73 + i, m, K) for i, m in enumerate(Ms)]
@@ -182,7 +190,7 @@ def test_api_pair_and_triple_match_single_gemvs():
     assert api.call("gemv_quant_triple", a) == rxq4.SUCCESS
     for yv, w in zip(ys, Wn):
         ref = orc.gemv_f32(w, K, x16)
-        assert util.f16_ulp_dist(host16(yv), orc.f32_to_fp16(ref)).max() <= 1
+        assert util.rounded_ok(host16(yv), ref).all()
 
 
 def test_api_gemv_pointer_resolution():
@@ -191,19 +199,19 @@ def test_api_gemv_pointer_resolution():
     M, K = 256, 2048
     Wn = util.weights(80, M, K)
     x16 = util.x_f16(81, K)
-    ref16 = orc.f32_to_fp16(orc.gemv_f32(Wn, K, x16))
+    ref = orc.gemv_f32(Wn, K, x16)
     W, x = dev(Wn), dev(x16)
     y = torch.empty(M, dtype=torch.float16, device="cuda")
     host_ptr = Wn.ctypes.data
     a = api.GemvQuantArgs(y=y.data_ptr(), weights=host_ptr, weights_device=W.data_ptr(),
                           ggml_type=12, x=x.data_ptr(), M=M, K=K)
     assert api.call("gemv_quant", a) == rxq4.SUCCESS
-    assert util.f16_ulp_dist(host16(y), ref16).max() <= 1
+    assert util.rounded_ok(host16(y), ref).all()
     y.zero_()
     a = api.GemvQuantArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=12, x=x.data_ptr(),
                           M=M, K=K)
     assert api.call("gemv_quant", a) == rxq4.SUCCESS
-    assert util.f16_ulp_dist(host16(y), ref16).max() <= 1
+    assert util.rounded_ok(host16(y), ref).all()
     a = api.GemvQuantArgs(y=y.data_ptr(), weights=host_ptr, ggml_type=12, x=x.data_ptr(),
                           M=M, K=K)
     assert api.call("gemv_quant", a) == rxq4.INVALID_ARGUMENT
@@ -262,7 +270,7 @@ def test_gemm_bf16(M, N, K):
     yb = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
     capi.gemm(yb, W, x, M, N, K)
     got = yb.view(torch.int16).cpu().numpy().view(np.uint16)
-    assert util.bf16_ulp_dist(got, util.f32_to_bf16_bits(ref.astype(np.float32))).max() <= util.ULPS_OUT
+    assert util.rounded_ok(got, ref, "bf16").all()
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 3, 2048), (2048, 16, 2048), (1000, 40, 2048),
@@ -279,7 +287,7 @@ def test_api_gemm_quant_batched_f16(M, N, K):
     assert api.call("gemm_quant_batched", a) == rxq4.SUCCESS
     got = f16(host16(y))
     assert util.rel_err(got, ref32) <= util.TOL
-    assert util.f16_ulp_dist(host16(y), orc.f32_to_fp16(ref64.astype(np.float32))).max() <= 1
+    assert util.rounded_ok(host16(y), ref64).all()
 
 
 def test_gemm_n1_is_the_gemv():

@@ -3,16 +3,17 @@
 Tolerance (stated once, used by every floating-point parity test):
   rel_err(y, ref) = max_i |y_i - ref_i| / max_i |ref_i|  <= TOL = 1e-3,
 where ref is the fp32 (or fp64) accumulation over identically rounded
-operands.  fp16/bf16 outputs are additionally required to lie within
-ULPS_OUT units in the last place of RNE(ref).  Dequantised weights and
-embedding rows are compared bit for bit.
+operands.  fp16/bf16 outputs must in addition be the round-to-nearest of a
+value within ACC_DELTA * max|ref| of ref (rounded_ok): the output rounding is
+exact and only the accumulation order may differ from the reference.
+Dequantised weights and embedding rows are compared bit for bit.
 """
 from __future__ import annotations
 
 import numpy as np
 
 TOL = 1e-3
-ULPS_OUT = 1
+ACC_DELTA = 1e-4
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -43,16 +44,32 @@ def rel_err(y, ref) -> float:
     return float(np.max(np.abs(y - ref)) / denom)
 
 
-def f16_ulp_dist(a_bits, b_bits) -> np.ndarray:
-    """Distance in fp16 ulps between two fp16 bit arrays (finite values)."""
-    def key(b):
-        b = np.asarray(b, dtype=np.int32)
-        return np.where(b & 0x8000, 0x8000 - (b & 0x7FFF), 0x8000 + (b & 0x7FFF))
-    return np.abs(key(a_bits) - key(b_bits))
+def bits_value(bits, kind: str) -> np.ndarray:
+    b = np.asarray(bits, dtype=np.uint16)
+    if kind == "f16":
+        return b.view(np.float16).astype(np.float64)
+    return (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def bf16_ulp_dist(a_bits, b_bits) -> np.ndarray:
-    return f16_ulp_dist(a_bits, b_bits)  # same sign-magnitude ordering trick on 16 bits
+def spacing(bits, kind: str) -> np.ndarray:
+    """Distance from |value| to the next larger representable magnitude."""
+    mag = np.asarray(bits, dtype=np.uint16) & 0x7FFF
+    nxt = np.minimum(mag + 1, 0x7BFF if kind == "f16" else 0x7F7F).astype(np.uint16)
+    return np.abs(bits_value(nxt, kind) - bits_value(mag, kind))
+
+
+def rounded_ok(y_bits, ref, kind: str = "f16", delta: float = ACC_DELTA,
+               extra=None) -> np.ndarray:
+    """True where the 16-bit output y is RNE of some z with |z - ref| <=
+    delta * max|ref|, i.e. |y - ref| <= spacing(y)/2 + delta * max|ref|
+    (+ `extra`, an additional per-element allowance such as a first rounding)."""
+    y = bits_value(y_bits, kind).reshape(np.shape(ref))
+    ref = np.asarray(ref, dtype=np.float64)
+    sp = np.maximum(spacing(y_bits, kind).reshape(ref.shape), 0)
+    allow = sp / 2 + delta * np.max(np.abs(ref))
+    if extra is not None:
+        allow = allow + extra
+    return np.abs(y - ref) <= allow * (1 + 1e-12)
 
 
 def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
