@@ -17,7 +17,7 @@
 //
 // GEMM kernel: workgroup = 4 waves; wave w owns 64 weight rows (4 fragments)
 // and all 16*TF tokens of the workgroup's token tile.  The x tile (16*TF
-// tokens x 64 k) is staged in LDS, double buffered, and read by all 4 waves;
+// tokens x 64 k) is staged in LDS, in a ring of 4 stages, and read by all 4 waves;
 // weights are dequantised straight into MFMA operand registers, so no wave
 // dequantises another wave's rows.  Flops per launch: 2*N*M*K.
 #include <stdlib.h>
@@ -119,16 +119,18 @@ __device__ __forceinline__ RowScales row_scales(u32x4 h) {
 // walked in stages of 64 (one 32-byte quant group il of a super-block = two
 // sub-blocks = two MFMA k-steps):
 //   * activations: each stage's TM x 64 tile is copied global -> LDS by the
-//     gfx950 direct-to-LDS loads (global_load_lds_dwordx4) into a ring of 4
-//     stage buffers, 3 stages ahead (issued right after the stage barrier,
-//     when every wave has finished reading the buffer being refilled).  Token t's 16-byte chunk c sits at
-//     position c ^ (t & 7) of the token's 128-byte row, so the fragment reads
+//     gfx950 direct-to-LDS loads (buffer_load_dwordx4 ... lds) into a ring
+//     of 4 stage buffers, 3 stages ahead (issued right after the stage
+//     barrier, when every wave has finished reading the buffer being
+//     refilled).  Token t's 16-byte chunk c sits at position c ^ (t & 7) of
+//     the token's 128-byte row, so the fragment reads
 //     (16 tokens x 16 bytes per k-group) hit distinct banks;
 //   * weights: each lane loads the 8 quant bytes of its fragment row three
 //     stages ahead (the block header two stages ahead) and dequantises them
 //     straight into MFMA operand registers, one stage ahead of use: the
-//     dequantisation of stage s+1 (VALU) is interleaved with the MFMAs of
-//     stage s (sched_group_barrier: 1 MFMA, 3 VALU), so the two pipes overlap;
+//     dequantisation of stage s+1 (VALU) is written between the MFMAs of
+//     stage s, one (fragment, half) per token fragment, so the two pipes
+//     overlap;
 //   * per stage: wait until this stage's copies have landed (vmcnt), one
 //     workgroup barrier, refill the freed buffer, then 2 x 4 x TF MFMAs.
 // The vmcnt bound is static: every stage issues the same loads (beyond the
@@ -154,14 +156,6 @@ struct GemmParams {
     int row_tiles, tok_tiles, splits, sb_per_split;
     int total_units, units_per_xcd;
 };
-
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 template <int YT>
 __device__ __forceinline__ void store4(void *y, int64_t idx, f32x4 v, bool vec_ok, int valid) {
@@ -218,20 +212,28 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     for (int f = 0; f < 4; ++f)
         wrow[f] = p.w + (int64_t)min(row_base + 16 * f + li, p.M - 1) * row_bytes + sb0 * kBlockBytes;
 
-    // Direct-to-LDS copy of stage s (clamped to the last stage).
+    // Direct-to-LDS copy of stage s (clamped to the last stage), as MUBUF
+    // buffer_load_dwordx4 ... lds over the workgroup's token rows (byte
+    // offsets < TM*K*2 <= 16 MiB).  The MUBUF form keeps the compiler's
+    // vmcnt bookkeeping for the register loads below exact; with the FLAT
+    // form (global_load_lds) it waits for vmcnt(0) at every use.
     const int ctok = lane >> 3;                 // token within a 1 KB chunk
     const int cpos = (lane & 7) ^ ctok;         // global 16-byte chunk this lane fetches
+    const __amdgpu_buffer_rsrc_t xrsrc =
+        make_rsrc(p.x + (int64_t)tok_base * K, min(TM, p.N - tok_base) * K * 2);
+    int xoff[kXLoads];
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) {
+        const int tok = min(8 * (wave + 4 * i) + ctok, p.N - 1 - tok_base);
+        xoff[i] = (tok * K + 8 * cpos) * 2;
+    }
     auto issue_x = [&](int s) {
         const int st = min(s, n_stages - 1);
-        const int k0 = (sb0 * 4 + st) * 64;
+        const int k0b = (sb0 * 4 + st) * 128;   // byte offset of the stage's 64 k
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i) {
             const int jc = wave + 4 * i;        // 1 KB chunk = 8 tokens
-            const int tok = min(tok_base + 8 * jc + ctok, p.N - 1);
-            const uint16_t *src = p.x + (int64_t)tok * K + k0 + 8 * cpos;
-            __builtin_amdgcn_global_load_lds(
-                (const void __attribute__((address_space(1))) *)src,
-                (void __attribute__((address_space(3))) *)&xs[s % kRing][jc * 1024], 16, 0, 0);
+            buffer_to_lds16(xrsrc, &xs[s % kRing][jc * 1024], xoff[i] + k0b);
         }
     };
     auto load_q = [&](int s, u32x2 *q) {
@@ -328,11 +330,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
                     else
                         anext[4 + f] = dequant8<XT>(qn[f].x, qn[f].y, true, rs.d * (float)(sc >> 8),
                                                     rs.dmin * (float)(mn >> 8));
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
-                    }
                 }
             }
             if (TF != 8) dequant_stage(qn, hn, (il + 1) & 3, anext);
@@ -518,9 +515,10 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     p.tok_tiles = (N + TM - 1) / TM;
     const int tiles = p.row_tiles * p.tok_tiles;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-    // Split K only when the tiles alone leave more than half of the CUs idle,
-    // then until the launch covers the CUs, keeping >= 2 super-blocks a split.
-    int splits = tiles * 2 >= cus ? 1 : (cus + tiles - 1) / tiles;
+    // Split K to the nearest whole number of launch waves over the CUs
+    // (cus / tiles rounded), keeping >= 2 super-blocks a split: 128 tiles on
+    // 256 CUs split 2, 172 tiles do not split.
+    int splits = std::max(1, (cus + tiles / 2) / tiles);
     splits = std::min(splits, std::max(1, p.nb / 2));
     splits = env_or("RXQ4_GEMM_SPLITS", splits);
     splits = std::max(1, std::min(splits, p.nb));

@@ -27,6 +27,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+
 namespace rxq4 {
 
 // The 64 activations of one slot, as fp16 pairs in nibble order, plus sums.
@@ -36,40 +38,42 @@ struct XSlot {
     float sx_lo, sx_hi;      // sum of the 32 low-nibble / high-nibble activations
 };
 
-// Load the slot (b, il) of x: elements b*256 + 64*il + [0, 64).  For quant
-// dword k (bytes 4k..4k+3 of the group) the pairs are
+// The slot (b, il) of x: elements b*256 + 64*il + [0, 64), as 8 x 16 bytes
+// (low-nibble half first).
+__device__ __forceinline__ void load_x_raw(const uint16_t *__restrict__ x, int b, int il,
+                                           u32x4 raw[8]) {
+    const uint16_t *base = x + b * kQK + 64 * il;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) raw[i] = load16(base + 8 * i);
+}
+
+// Permute a raw slot into pairs and sums.  For quant dword k (bytes 4k..4k+3
+// of the group) the pairs are
 //   p[4k+0] = (x_lo[4k],   x_lo[4k+2])   p[4k+1] = (x_lo[4k+1], x_lo[4k+3])
 //   p[4k+2] = (x_hi[4k],   x_hi[4k+2])   p[4k+3] = (x_hi[4k+1], x_hi[4k+3])
 // matching (q & 0x000F000F) and ((q >> 8) & 0x000F000F) (and 0x00F000F0).
-__device__ __forceinline__ void load_x_slot(const uint16_t *__restrict__ x, int b, int il,
-                                            bool valid, XSlot &s) {
+// Pairs are byte permutes; the sums are dot products with (1, 1) (exact
+// products, fp32 accumulation).
+__device__ __forceinline__ void x_slot_from_raw(const u32x4 raw[8], XSlot &s) {
     uint32_t xl[16], xh[16];
-    if (valid) {
-        const uint16_t *base = x + b * kQK + 64 * il;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4 lo = load16(base + 8 * i);
-            const u32x4 hi = load16(base + 32 + 8 * i);
-            xl[4 * i + 0] = lo.x; xl[4 * i + 1] = lo.y; xl[4 * i + 2] = lo.z; xl[4 * i + 3] = lo.w;
-            xh[4 * i + 0] = hi.x; xh[4 * i + 1] = hi.y; xh[4 * i + 2] = hi.z; xh[4 * i + 3] = hi.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) { xl[i] = 0; xh[i] = 0; }
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 lo = raw[i], hi = raw[4 + i];
+        xl[4 * i + 0] = lo.x; xl[4 * i + 1] = lo.y; xl[4 * i + 2] = lo.z; xl[4 * i + 3] = lo.w;
+        xh[4 * i + 0] = hi.x; xh[4 * i + 1] = hi.y; xh[4 * i + 2] = hi.z; xh[4 * i + 3] = hi.w;
     }
+    const half2_t ones = as_half2(0x3C003C00u);
     float sl = 0.0f, sh = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const uint32_t a = xl[2 * k], c = xl[2 * k + 1];
-        s.p[4 * k + 0] = (a & 0xFFFFu) | (c << 16);
-        s.p[4 * k + 1] = (a >> 16) | (c & 0xFFFF0000u);
-        const uint32_t e = xh[2 * k], f = xh[2 * k + 1];
-        s.p[4 * k + 2] = (e & 0xFFFFu) | (f << 16);
-        s.p[4 * k + 3] = (e >> 16) | (f & 0xFFFF0000u);
-        sl += f16_bits_to_f32(a) + f16_bits_to_f32(a >> 16) + f16_bits_to_f32(c) +
-              f16_bits_to_f32(c >> 16);
-        sh += f16_bits_to_f32(e) + f16_bits_to_f32(e >> 16) + f16_bits_to_f32(f) +
-              f16_bits_to_f32(f >> 16);
+        s.p[4 * k + 0] = __builtin_amdgcn_perm(xl[2 * k + 1], xl[2 * k], 0x05040100u);
+        s.p[4 * k + 1] = __builtin_amdgcn_perm(xl[2 * k + 1], xl[2 * k], 0x07060302u);
+        s.p[4 * k + 2] = __builtin_amdgcn_perm(xh[2 * k + 1], xh[2 * k], 0x05040100u);
+        s.p[4 * k + 3] = __builtin_amdgcn_perm(xh[2 * k + 1], xh[2 * k], 0x07060302u);
+        sl = __builtin_amdgcn_fdot2(as_half2(xl[2 * k]), ones, sl, false);
+        sh = __builtin_amdgcn_fdot2(as_half2(xh[2 * k]), ones, sh, false);
+        sl = __builtin_amdgcn_fdot2(as_half2(xl[2 * k + 1]), ones, sl, false);
+        sh = __builtin_amdgcn_fdot2(as_half2(xh[2 * k + 1]), ones, sh, false);
     }
     s.sx_lo = sl;
     s.sx_hi = sh;
@@ -105,6 +109,27 @@ __device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t m
     return r;
 }
 
+// Raw dot products of one quant group (32 bytes q0, q1) with its slot of x:
+// acc_lo += sum (1024 + q_lo) x_lo, acc_hi += sum (1024 + 16 q_hi) x_hi.
+__device__ __forceinline__ void group_dot(u32x4 q0, u32x4 q1, const XSlot &s, uint32_t magic,
+                                          float &acc_lo, float &acc_hi) {
+    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        // the four pairs first: a dot product right behind the VALU op that
+        // wrote its operand costs a wait state on gfx950
+        const uint32_t v = q[k], v8 = q[k] >> 8;
+        const uint32_t w0 = and_or(v, 0x000F000Fu, magic);
+        const uint32_t w1 = and_or(v8, 0x000F000Fu, magic);
+        const uint32_t w2 = and_or(v, 0x00F000F0u, magic);
+        const uint32_t w3 = and_or(v8, 0x00F000F0u, magic);
+        acc_lo = __builtin_amdgcn_fdot2(as_half2(w0), as_half2(s.p[4 * k + 0]), acc_lo, false);
+        acc_hi = __builtin_amdgcn_fdot2(as_half2(w2), as_half2(s.p[4 * k + 2]), acc_hi, false);
+        acc_lo = __builtin_amdgcn_fdot2(as_half2(w1), as_half2(s.p[4 * k + 1]), acc_lo, false);
+        acc_hi = __builtin_amdgcn_fdot2(as_half2(w3), as_half2(s.p[4 * k + 3]), acc_hi, false);
+    }
+}
+
 // Partial dot product of one slot of one row.
 __device__ __forceinline__ float slot_dot(u32x4 hdr, u32x4 q0, u32x4 q1, const XSlot &s,
                                           const ScaleDecode &sd, uint32_t magic) {
@@ -112,20 +137,8 @@ __device__ __forceinline__ float slot_dot(u32x4 hdr, u32x4 q0, u32x4 q1, const X
     const float dmin = f16_bits_to_f32(hdr.x >> 16);
     const uint32_t sc = ((hdr.y >> sd.shA) & sd.mA) | ((hdr.w >> sd.shC) & sd.mC);
     const uint32_t mn = ((hdr.z >> sd.shA) & sd.mA) | ((hdr.w >> sd.shC4) & sd.mC);
-    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     float acc_lo = s.bias_lo, acc_hi = s.bias_hi;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t v = q[k], v8 = q[k] >> 8;
-        acc_lo = __builtin_amdgcn_fdot2(as_half2(and_or(v, 0x000F000Fu, magic)),
-                                        as_half2(s.p[4 * k + 0]), acc_lo, false);
-        acc_lo = __builtin_amdgcn_fdot2(as_half2(and_or(v8, 0x000F000Fu, magic)),
-                                        as_half2(s.p[4 * k + 1]), acc_lo, false);
-        acc_hi = __builtin_amdgcn_fdot2(as_half2(and_or(v, 0x00F000F0u, magic)),
-                                        as_half2(s.p[4 * k + 2]), acc_hi, false);
-        acc_hi = __builtin_amdgcn_fdot2(as_half2(and_or(v8, 0x00F000F0u, magic)),
-                                        as_half2(s.p[4 * k + 3]), acc_hi, false);
-    }
+    group_dot(q0, q1, s, magic, acc_lo, acc_hi);
     const float d_lo = d * (float)(sc & 0xFFu);
     const float d_hi = (d * 0.0625f) * (float)((sc >> 8) & 0xFFu);
     const float m_lo = dmin * (float)(mn & 0xFFu);
@@ -133,8 +146,8 @@ __device__ __forceinline__ float slot_dot(u32x4 hdr, u32x4 q0, u32x4 q1, const X
     return d_lo * acc_lo - m_lo * s.sx_lo + (d_hi * acc_hi - m_hi * s.sx_hi);
 }
 
-// DPP control words (GFX9): row_ror:n = 0x120 + n, row_bcast:15 = 0x142,
-// row_bcast:31 = 0x143.
+// DPP control words (GFX9): quad_perm = 0x00-0xFF, row_ror:n = 0x120 + n,
+// row_half_mirror = 0x141, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_add(float v) {
     const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
@@ -142,8 +155,8 @@ __device__ __forceinline__ float dpp_add(float v) {
     return v + __builtin_bit_cast(float, moved);
 }
 
-// Sum over aligned groups of W lanes (W in {4, 8, 16, 32, 64}).  The full sum
-// is valid in lane W-1 of every group (and in every lane of the group for
+// Sum over aligned groups of W lanes (W in {2, 4, 8, 16, 32, 64}).  The full
+// sum is valid in lane W-1 of every group (and in every lane of the group for
 // W <= 16).
 template <int W>
 __device__ __forceinline__ float lane_group_sum(float v) {
@@ -155,8 +168,9 @@ __device__ __forceinline__ float lane_group_sum(float v) {
         if (W >= 32) v = dpp_add<0x142, 0xA>(v);  // rows 1, 3 += last lane of rows 0, 2
         if (W >= 64) v = dpp_add<0x143, 0xC>(v);  // rows 2, 3 += lane 31
     } else {
-#pragma unroll
-        for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        v = dpp_add<0xB1, 0xF>(v);                // quad_perm [1,0,3,2]
+        if (W >= 4) v = dpp_add<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+        if (W >= 8) v = dpp_add<0x141, 0xF>(v);   // row_half_mirror
     }
     return v;
 }
@@ -170,6 +184,7 @@ struct Range {
     const uint16_t *res;
     int rows;
     int first_unit;
+    int n_units;
 };
 
 __device__ __forceinline__ Range range_of_unit(const GemvParams &p, int unit) {
@@ -185,11 +200,13 @@ __device__ __forceinline__ Range range_of_unit(const GemvParams &p, int unit) {
     r.res = ri == 0 ? r0 : (ri == 1 ? r1 : r2);
     r.rows = ri == 0 ? m0 : (ri == 1 ? m1 : m2);
     r.first_unit = ri == 0 ? 0 : (ri == 1 ? u1 : u2);
+    r.n_units = (ri == 0 ? u1 : (ri == 1 ? u2 : p.total_units)) - r.first_unit;
     return r;
 }
 
+// `res` is the fp16 residual of the row (kEpiAdd), loaded with the weights.
 template <int EPI>
-__device__ __forceinline__ void store_row(const Range &r, int row, float v) {
+__device__ __forceinline__ void store_row(const Range &r, int row, float v, uint32_t res) {
     if (EPI == kEpiF32) {
         static_cast<float *>(r.y)[row] = v;
     } else if (EPI == kEpiF16) {
@@ -197,8 +214,7 @@ __device__ __forceinline__ void store_row(const Range &r, int row, float v) {
     } else {
         // q4_gemm.cu:774-777: round the projection, add the residual, round.
         const float projected = f16_bits_to_f32(f32_to_f16_bits(v));
-        static_cast<uint16_t *>(r.y)[row] =
-            f32_to_f16_bits(projected + f16_bits_to_f32(r.res[row]));
+        static_cast<uint16_t *>(r.y)[row] = f32_to_f16_bits(projected + f16_bits_to_f32(res));
     }
 }
 
@@ -208,27 +224,47 @@ __device__ __forceinline__ uint32_t magic_vgpr() {
     return m;
 }
 
+// U items of weights in flight: header, the slot's 32 quant bytes and, for
+// kEpiAdd, the fp16 residual of the item's row.
 template <int U>
 struct Batch {
     u32x4 h[U], a[U], c[U];
+    uint32_t r[U];
 };
 
 // ---------------------------------------------------------------------------
-// Register kernel: a row has LPR = 4*nb <= 64 slots (nb in {1,2,4,8,16}), so a
-// wave covers RPS = 64/LPR rows per step and each lane's slot never changes.
-// Wave w serves steps [t0, t1) of one range; batches of U steps are loaded one
-// batch ahead of the arithmetic.
+// Register kernel: a lane owns one slot (64 weights: quant group il of block
+// b) of a row; a row has LPR = 4*nb <= 64 slots (nb in {1,2,4,8,16}), so a
+// wave covers RPS = 64/LPR rows per step and each lane's slot never changes;
+// its 64 activations stay in VGPRs.  Wave w serves the contiguous steps
+// [t0, t1) of one range, at most 256 rows (per_unit * RPS <= 256).
+//   * x (K <= 4096 fp16) is copied into LDS once per workgroup with one
+//     direct-to-LDS load per thread and round, ahead of the weights; each
+//     lane then reads its slot from LDS.
+//   * Two batches of U steps are issued right behind x, so a wave with at
+//     most 2U steps makes a single memory round trip; longer waves refill
+//     each buffer as soon as it has been consumed.
+//   * Row results collect in LDS and leave in coalesced stores of 64 rows;
+//     the residuals (kEpiAdd) of the first 64 were fetched up front.
+constexpr int kRegMaxK = 4096;
+constexpr int kRegMaxRows = 256;
+
 template <int LPR, int EPI, int U>
 __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
     constexpr int RPS = 64 / LPR;
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (wave >= p.total_units) return;
-    const Range rg = range_of_unit(p, wave);
+    __shared__ __attribute__((aligned(16))) uint16_t xsh[kRegMaxK];
+    __shared__ float outs[4][kRegMaxRows];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = blockIdx.x * 4 + wv;
+    const bool active = wave < p.total_units;
+    const Range rg = range_of_unit(p, active ? wave : 0);
     const int n_steps = (rg.rows + RPS - 1) / RPS;
-    const int t0 = (wave - rg.first_unit) * p.per_unit;
-    const int t1 = min(t0 + p.per_unit, n_steps);
-    if (t0 >= t1) return;
+    const int t0 = active ? (wave - rg.first_unit) * p.per_unit : 0;
+    const int t1 = active ? min(t0 + p.per_unit, n_steps) : 0;
+    const int row0 = t0 * RPS;
+    const int last = rg.rows - 1;
 
     const int slot = lane & (LPR - 1);
     const int sub = lane / LPR;
@@ -236,12 +272,24 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
     const uint32_t row_bytes = (uint32_t)p.nb * kBlockBytes;
     const uint32_t hdr_off = (uint32_t)b * kBlockBytes;
     const uint32_t q_off = hdr_off + 16u + 32u * (uint32_t)il;
-    const int last = rg.rows - 1;
 
+    // x -> LDS: chunk c (16 bytes) of thread c + 256*round; chunks past K
+    // read as zeros.
+    const int x_bytes = p.nb * kQK * 2;
+    const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(p.x, x_bytes);
+    constexpr int kXRounds = (RPS == 1) ? 2 : 1;  // K = 4096 only with LPR = 64
+#pragma unroll
+    for (int r = 0; r < kXRounds; ++r)
+        buffer_to_lds16(xrsrc, &xsh[(256 * r + 64 * wv) * 8], (256 * r + tid) * 16);
+    __builtin_amdgcn_sched_barrier(0);  // the counted loads below stay behind the copies
+
+    // Weights.  Steps past t1 reload step t1-1 (inactive waves: step 0; L2
+    // hits, results discarded): the loads stay unconditional, so the
+    // compiler's vmcnt waits count them exactly.
     auto load = [&](int t, Batch<U> &bt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int ts = min(t + u, t1 - 1);
+            const int ts = max(0, min(t0 + t + u, t1 - 1));
             // uniform part: first row of the step; lane part: sub-row, clamped
             const uint8_t *base = rg.w + (int64_t)(ts * RPS) * row_bytes;
             const uint32_t lrow = (uint32_t)min(sub, last - ts * RPS) * row_bytes;
@@ -250,30 +298,60 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
             bt.c[u] = load16(base + (lrow + q_off + 16u));
         }
     };
-    // First weight batch goes out before the activations, so the two memory
-    // round trips overlap.
     Batch<U> A, B;
-    load(t0, A);
+    load(0, A);
+    load(U, B);
+    // residual of row row0 + lane (kEpiAdd)
+    uint32_t res = 0;
+    if (EPI == kEpiAdd) res = rg.res[min(row0 + lane, last)];
+    constexpr int kWeightLoads = 2 * U * 3 + (EPI == kEpiAdd ? 1 : 0);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<kWeightLoads>();  // this wave's x copies have landed
+    lds_barrier();               // ... and every other wave's
+
+    u32x4 xraw[8];
+    const u32x4 *xs16 = reinterpret_cast<const u32x4 *>(xsh) + b * 32 + il * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xraw[i] = xs16[i];
     XSlot xs;
-    load_x_slot(p.x, b, il, true, xs);
+    x_slot_from_raw(xraw, xs);
     const ScaleDecode sd = scale_decode_for(il);
     const uint32_t magic = magic_vgpr();
+    const int n = t1 - t0;
     auto compute = [&](int t, const Batch<U> &bt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float v = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic);
-            v = lane_group_sum<LPR>(v);
-            const int row = (t + u) * RPS + sub;
-            if (slot == LPR - 1 && t + u < t1 && row < rg.rows) store_row<EPI>(rg, row, v);
+            if (t + u < n) {  // uniform
+                float v = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic);
+                v = lane_group_sum<LPR>(v);
+                if (slot == LPR - 1) outs[wv][(t + u) * RPS + sub] = v;
+            }
         }
     };
 
-    for (int t = t0; t < t1; t += 2 * U) {
-        if (t + U < t1) load(t + U, B);
+    // Steady state: A holds steps [t, t+U), B [t+U, t+2U), both in flight;
+    // each is refilled right after it has been consumed.  The refills are
+    // unconditional, so the loop entry and back edge have the same loads
+    // outstanding in the same order (exact vmcnt waits).  The tail computes
+    // the last <= 2U steps with no loads behind them.
+    int t = 0;
+    for (; t + 2 * U < n; t += 2 * U) {
         compute(t, A);
-        if (t + U >= t1) break;
-        if (t + 2 * U < t1) load(t + 2 * U, A);
+        load(t + 2 * U, A);
         compute(t + U, B);
+        load(t + 3 * U, B);
+    }
+    compute(t, A);
+    compute(t + U, B);
+
+    // Coalesced stores of the wave's rows (same-wave LDS traffic is in
+    // order, so the results written above are visible here).
+    const int rows = min(n * RPS, rg.rows - row0);
+    if (lane < rows) store_row<EPI>(rg, row0 + lane, outs[wv][lane], res);
+    for (int r = 64; r < rows; r += 64) {
+        const int row = row0 + r + lane;
+        if (r + lane < rows)
+            store_row<EPI>(rg, row, outs[wv][r + lane], EPI == kEpiAdd ? rg.res[row] : 0u);
     }
 }
 
@@ -281,9 +359,11 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 // LDS kernel for rows with more than 64 slots (any K): the workgroup stages
 // x once in LDS in the same permuted-pair layout (36 dwords per slot), and
 // each wave owns whole rows, walking a row's slots 64 at a time
-// (J = ceil(4*nb/64) items per row).  Items (row, j) are processed U at a
-// time with the next batch of weights in flight; the row's lanes are summed
-// once per row.  No barrier after the staging barrier.
+// (J = ceil(4*nb/64) items per row).  Two batches of U items (and the
+// residuals of their rows) are issued right after the first round of x
+// loads, so the staging overlaps the weight round trip; each buffer is
+// refilled as soon as it has been consumed.  The row's lanes are summed once per row.  No
+// barrier after the staging barrier.
 constexpr int kLdsSlotWords = 36;
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
@@ -302,45 +382,61 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
     const int n_items = (r1 > r0 ? r1 - r0 : 0) * J;
     const uint32_t row_bytes = (uint32_t)p.nb * kBlockBytes;
 
-    // Items are walked in order by two cursors (loads run one batch ahead of
-    // the arithmetic): item (row, j) covers slots [64j, 64j+64) of the row.
+    // Items are walked in order by two cursors (loads run up to two batches
+    // ahead of the arithmetic): item (row, j) covers slots [64j, 64j+64).
+    // Items past the end reload the last row (inactive waves: row 0 of the
+    // range) and are discarded: the loads stay unconditional, so the
+    // compiler's vmcnt waits count them exactly.
     int ld_row = r0, ld_j = 0;
     auto load = [&](Batch<U> &bt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int row = min(ld_row, r1 - 1);
+            const int row = max(0, min(ld_row, r1 - 1));
             const int slot = min(64 * ld_j + lane, n_slots - 1);
             const uint8_t *blk = rg.w + (int64_t)row * row_bytes + (slot >> 2) * kBlockBytes;
             bt.h[u] = load16(blk);
             bt.a[u] = load16(blk + 16 + 32 * (slot & 3));
             bt.c[u] = load16(blk + 32 + 32 * (slot & 3));
+            if (EPI == kEpiAdd) bt.r[u] = rg.res[row];
             if (++ld_j == J) { ld_j = 0; ++ld_row; }
         }
     };
-    Batch<U> A, B;
-    if (n_items > 0) load(A);
-
-    // Stage x: one slot per thread and round.
-    for (int s = threadIdx.x; s < n_slots; s += blockDim.x) {
+    // Stage x, one slot per thread and round; the first round's loads go out
+    // before the weights (vector loads complete in order).
+    auto stage = [&](int s, const u32x4 raw[8]) {
         XSlot xs;
-        load_x_slot(p.x, s >> 2, s & 3, true, xs);
+        x_slot_from_raw(raw, xs);
         uint32_t *dst = xlds + s * kLdsSlotWords;
 #pragma unroll
         for (int k = 0; k < 8; ++k)
             *reinterpret_cast<u32x4 *>(dst + 4 * k) =
                 u32x4{xs.p[4 * k], xs.p[4 * k + 1], xs.p[4 * k + 2], xs.p[4 * k + 3]};
         *reinterpret_cast<f32x4v *>(dst + 32) = f32x4v{xs.bias_lo, xs.bias_hi, xs.sx_lo, xs.sx_hi};
+    };
+    const int s_first = threadIdx.x;
+    const int s_load = min(s_first, n_slots - 1);
+    u32x4 xraw[8];
+    load_x_raw(p.x, s_load >> 2, s_load & 3, xraw);
+    __builtin_amdgcn_sched_barrier(0);
+    Batch<U> A, B;
+    load(A);
+    load(B);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s_first < n_slots) stage(s_first, xraw);
+    for (int s = s_first + blockDim.x; s < n_slots; s += blockDim.x) {
+        load_x_raw(p.x, s >> 2, s & 3, xraw);
+        stage(s, xraw);
     }
     __syncthreads();
     if (n_items == 0) return;
 
     const uint32_t magic = magic_vgpr();
     float acc = 0.0f;
-    int cp_row = r0, cp_j = 0;
+    int cp_item = 0, cp_row = r0, cp_j = 0;
     auto compute = [&](const Batch<U> &bt) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (cp_row < r1) {  // uniform
+            if (cp_item < n_items) {  // uniform
                 const int slot = 64 * cp_j + lane;
                 const bool valid = slot < n_slots;
                 const int sl = valid ? slot : 0;
@@ -359,9 +455,10 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
                 const ScaleDecode sd = scale_decode_for(sl & 3);
                 const float v = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic);
                 acc += valid ? v : 0.0f;
+                ++cp_item;
                 if (++cp_j == J) {
                     const float total = lane_group_sum<64>(acc);
-                    if (lane == 63) store_row<EPI>(rg, cp_row, total);
+                    if (lane == 63) store_row<EPI>(rg, cp_row, total, bt.r[u]);
                     acc = 0.0f;
                     cp_j = 0;
                     ++cp_row;
@@ -369,13 +466,17 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
             }
         }
     };
-    for (int i = 0; i < n_items; i += 2 * U) {
-        if (i + U < n_items) load(B);
+    // Steady state with unconditional refills, then the last <= 2U items
+    // (the register kernel's scheme: exact vmcnt waits).
+    int i = 0;
+    for (; i + 2 * U < n_items; i += 2 * U) {
         compute(A);
-        if (i + U >= n_items) break;
-        if (i + 2 * U < n_items) load(A);
+        load(A);
         compute(B);
+        load(B);
     }
+    compute(A);
+    compute(B);
 }
 
 const DeviceInfo &device_info() {
@@ -420,9 +521,15 @@ static int assign_units(GemvParams &p, int rows_per_item, int per_unit) {
     return units;
 }
 
+// Steps per load batch of the register kernel (two batches are in flight).
+#ifndef RXQ4_GEMV_BATCH
+#define RXQ4_GEMV_BATCH 2
+#endif
+constexpr int kRegBatch = RXQ4_GEMV_BATCH;
+
 template <int LPR, int EPI>
 static void launch_reg(const GemvParams &p, int grid, hipStream_t st) {
-    gemv_reg_kernel<LPR, EPI, 2><<<grid, 256, 0, st>>>(p);
+    gemv_reg_kernel<LPR, EPI, kRegBatch><<<grid, 256, 0, st>>>(p);
 }
 
 template <int EPI>
@@ -433,9 +540,9 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         // Register kernel: aim for `waves_per_cu` waves per CU over the launch.
         const int rps = 64 / slots;
         const int64_t steps = (p.total_rows + rps - 1) / rps;
-        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_WAVES_PER_CU", 8);
+        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_WAVES_PER_CU", 4);
         int per_wave = (int)((steps + target - 1) / target);
-        if (per_wave < 1) per_wave = 1;
+        per_wave = std::max(1, std::min(per_wave, kRegMaxRows / rps));
         const int waves = assign_units(p, rps, per_wave);
         const int grid = (waves + 3) / 4;
         switch (slots) {
@@ -449,7 +556,7 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         // LDS kernel: whole rows per wave, `waves_per_cu` waves per CU.
         const size_t lds = (size_t)slots * kLdsSlotWords * sizeof(uint32_t);
         if (lds > 160 * 1024) return hipErrorInvalidValue;
-        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_LDS_WAVES_PER_CU", 8);
+        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_LDS_WAVES_PER_CU", 4);
         int per_wave = (int)((p.total_rows + target - 1) / target);
         if (per_wave < 1) per_wave = 1;
         const int waves = assign_units(p, 1, per_wave);

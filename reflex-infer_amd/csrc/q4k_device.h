@@ -86,4 +86,29 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Workgroup barrier without the fence of __syncthreads (which waits for all
+// outstanding vector memory operations); callers wait for what they need.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Buffer resource over `bytes` bytes at `base` (raw buffer, no swizzle);
+// loads past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes,
+                                             0x00020000);
+}
+
+// 16 bytes per lane, global (rsrc + voffset) -> LDS at lds + 16 * lane.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds,
+                                                int voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rsrc, (void __attribute__((address_space(3))) *)lds, 16, voffset, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (lgkmcnt and expcnt untouched).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 }  // namespace rxq4
