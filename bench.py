@@ -13,8 +13,11 @@ A step is one pass over all 36 layers (144 launches); `value` is algorithmic
 bytes per step / seconds per step.  Inputs are resident in HBM; the 1.56 GB
 of weights exceed the 256 MB Infinity Cache, so every step streams from HBM.
 
-Also reported, each on the stream it runs on with HIP events:
-  roofline     the dominant kernel (gate+up pair GEMV), per-launch duration
+Also reported, each as n launches captured in a HIP graph on the bench
+stream and timed with HIP events recorded on that stream around replays:
+  roofline     the dominant kernel (gate+up pair GEMV), per-launch duration;
+               `traffic` comes from the committed rocprofv3 PMC summary
+               (FETCH_SIZE + WRITE_SIZE scaled by a copy of known size)
   per_kernel   every decode projection, the LM head [151936 x 2048] fp32
                GEMV, the 4096-id Zipf(1.1) embedding gather, and the prefill
                GEMM at m=512 (TFLOP/s, BASELINE metric's second half)
@@ -50,6 +53,23 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_gate_up_pair_decode36.txt")
+
+
+def measured_traffic():
+    """HBM bytes per gate+up launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain
+    copy of known size); (None, None) when the summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].split()[0]), os.path.relpath(TRAFFIC_FILE, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -58,6 +78,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip LM head / embedding / GEMM")
     ap.add_argument("--eager", action="store_true", help="time eager launches, not a graph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device copy (PMC byte-counter calibration)")
     return ap.parse_args()
 
 
@@ -75,9 +97,20 @@ def main() -> int:
     import rxq4
     from rxq4 import api, capi
 
-    rxq4.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        # A plain copy of known size: what FETCH_SIZE / WRITE_SIZE read for
+        # it calibrates the byte counters of the kernels profiled beside it.
+        a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)  # 256 MiB
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": a.numel() * 4,
+                          "bytes_written": b.numel() * 4, "copies": 3}), flush=True)
+        return 0
+    rxq4.load()
     stream = torch.cuda.Stream()
     sp = stream.cuda_stream
 
@@ -198,21 +231,33 @@ def main() -> int:
     eager_ms = (time.perf_counter() - t0) * 1e3 / 3
 
     # ------------------------------------------------ per-kernel durations
-    def per_launch(launch, n, warm=3):
-        """Mean duration of `launch(i)` bracketed by events on `stream`."""
+    def per_launch(launch, n, reps=5):
+        """Duration of one `launch(i)` as the decode graph issues it: n
+        launches (distinct weights) captured in a HIP graph on `stream` and
+        replayed `reps` times between events recorded on `stream`; returns
+        the median and mean over the replays of elapsed / n, in us."""
         with torch.cuda.stream(stream):
-            for i in range(warm):
+            for i in range(3):
                 launch(i)
         torch.cuda.synchronize()
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-        with torch.cuda.stream(stream):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="relaxed"):
             for i in range(n):
-                starts[i].record(stream)
                 launch(i)
-                ends[i].record(stream)
+        with torch.cuda.stream(stream):
+            g.replay()
         torch.cuda.synchronize()
-        d = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))  # us
+        d = []
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                e0.record(stream)
+                g.replay()
+                e1.record(stream)
+            torch.cuda.synchronize()
+            d.append(e0.elapsed_time(e1) * 1e3 / n)
+        del g
         return float(np.median(d)), float(np.mean(d))
 
     kernels = {}
@@ -228,9 +273,11 @@ def main() -> int:
     med, mean = per_launch(gu_launch, R)
     gu_bytes = qbytes(2 * FFN, HIDDEN) + 2 * HIDDEN + 2 * 2 * FFN
     kernels["gate_up_pair_22016x2048"] = {"us": round(med, 3), "GBps": round(gu_bytes / med / 1e3, 1)}
+    traffic, traffic_src = measured_traffic()
     roofline = {"bound": "hbm", "achieved": round(gu_bytes / med / 1e3, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(gu_bytes / med / 1e3 / HBM_PEAK_GBS, 4),
-                "traffic": None, "kernel": "gemv_reg_kernel<32,F16> (gate+up pair)",
+                "traffic": traffic, "traffic_source": traffic_src,
+                "kernel": "gemv_reg_kernel<32,F16,2> (gate+up pair)",
                 "bytes_per_launch": gu_bytes, "us_per_launch": round(med, 3),
                 "us_mean": round(mean, 3)}
 

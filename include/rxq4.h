@@ -18,7 +18,11 @@
  *   - fp16/bf16 buffers are raw 16-bit patterns; x must be 16-byte aligned.
  *   - K must be a positive multiple of 256 and at most RXQ4_MAX_K.
  *   - `stream` is a hipStream_t (NULL = null stream).  Calls only enqueue
- *     work; nothing synchronises and nothing allocates device memory.
+ *     work and nothing synchronises.  Nothing allocates device memory except
+ *     the GEMM entry points when they split K over workgroups (few output
+ *     tiles, e.g. M = 2048 at N <= 2048): they keep one fp32 partial-sum
+ *     workspace per device, allocated on first use and grown when a larger
+ *     one is needed (tiles * splits * 128 KiB), and held until exit.
  *   - The return value is a reflex::infer::Status value (RXQ4_STATUS_*).
  *     On an error nothing is launched; rxq4_last_error() says why.
  */

@@ -5,7 +5,10 @@
   * the library defines every public symbol the reference's dispatcher
     defines and every kernel-seam symbol it needs
     (reference src/dispatch.cpp, src/kernels/kernel_entrypoints.h:7-16);
-  * the library exports every entry point declared in include/rxq4.h.
+  * the library exports every entry point declared in include/rxq4.h;
+  * the reference's own dispatcher (src/dispatch.cpp compiled from its
+    sources) links against the kernels-only library and its calls land in
+    this build's seam (statuses the seam returns before any GPU work).
 """
 from __future__ import annotations
 
@@ -62,6 +65,23 @@ def test_library_satisfies_reference_dispatcher_symbols():
     assert len(defined) == 11 and len(needed) == 9
     assert defined <= set(ours), defined - set(ours)
     assert needed <= set(ours), needed - set(ours)
+
+
+KLIB = os.path.join(ROOT, "reflex-infer_amd", "lib", "libreflex_infer_hip_kernels.so")
+DISPATCH_ON_HIP = os.path.join(ORACLE, "_ref", "dispatch_on_hip")
+
+
+@pytest.mark.skipif(not (HAVE_REF or os.path.exists(DISPATCH_ON_HIP)),
+                    reason="reference checkout not present and probe not prebuilt")
+def test_reference_dispatcher_runs_on_this_kernel_layer():
+    if HAVE_REF:
+        _make("_ref/dispatch_on_hip")
+    ours = _nm(KLIB, "-D", "--defined-only")
+    assert not any("reflex5infer10gemv_quantE" in s for s in ours)  # seam only, no API
+    out = _probe(DISPATCH_ON_HIP)
+    # Q5_K through the reference dispatcher -> this seam: UnsupportedQuantFormat;
+    # attention -> this seam's NotImplemented; nothing registered.
+    assert out == {"gemv_quant_q5k": 3, "flash_attention_decode": 5, "registry_empty": 1}
 
 
 def test_library_exports_every_c_abi_entry_point():
