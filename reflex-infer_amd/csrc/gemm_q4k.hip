@@ -17,7 +17,7 @@
 //
 // GEMM kernel: workgroup = 4 waves; wave w owns 64 weight rows (4 fragments)
 // and all 16*TF tokens of the workgroup's token tile.  The x tile (16*TF
-// tokens x 64 k) is staged in LDS, in a ring of 4 stages, and read by all 4 waves;
+// tokens x 64 k) is staged in LDS, in a ring of 5 stages, and read by all 4 waves;
 // weights are dequantised straight into MFMA operand registers, so no wave
 // dequantises another wave's rows.  Flops per launch: 2*N*M*K.
 #include <stdlib.h>
@@ -34,6 +34,7 @@ namespace rxq4 {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -69,17 +70,40 @@ __device__ __forceinline__ void dequant4(uint32_t m, float scale, float dm, uint
     out[1] = pack2<XT>(w2, w3);
 }
 
-// Eight weights from the low (hi = false) or high nibbles of bytes v0, v1.
-// High nibbles are used in place (16*q) with dsc/16, an exact rescaling.
+// Two weights from bytes b, b+1 of m (nibble values, or 16 x nibble values
+// with scale = d*sc/16), packed: w = scale*byte - dm, one fp32 rounding.
 template <int XT>
-__device__ __forceinline__ u32x4 dequant8(uint32_t v0, uint32_t v1, bool hi, float dsc,
+__device__ __forceinline__ uint32_t dq_pair(uint32_t m, int b, float scale, float dm) {
+    const float w0 = scale * (float)((m >> (8 * b)) & 0xFFu) - dm;
+    const float w1 = scale * (float)((m >> (8 * b + 8)) & 0xFFu) - dm;
+    return pack2<XT>(w0, w1);
+}
+
+// Eight weights from the low (hi = false) or high nibbles of bytes v0, v1.
+// High nibbles are used in place (16*q): the caller passes scale = d*sc/16
+// for them, an exact rescaling.
+template <int XT>
+__device__ __forceinline__ u32x4 dequant8(uint32_t v0, uint32_t v1, bool hi, float scale,
                                           float dm) {
     const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-    const float scale = hi ? dsc * 0.0625f : dsc;
     uint32_t o[4];
     dequant4<XT>(mask_opaque(v0, mask), scale, dm, o);
     dequant4<XT>(mask_opaque(v1, mask), scale, dm, o + 2);
     return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// Scales of one weight row for quant group il: sub-block 2il (low nibbles)
+// and 2il+1 (high nibbles, scale pre-divided by 16).
+struct GroupScales {
+    float lo, hi, dm_lo, dm_hi;
+};
+
+__device__ __forceinline__ GroupScales group_scales(u32x4 h, int il) {
+    const float d = f16_bits_to_f32(h.x & 0xFFFFu), dmin = f16_bits_to_f32(h.x >> 16);
+    uint32_t sc, mn;
+    scale_pair(h.y, h.z, h.w, il, &sc, &mn);
+    return GroupScales{d * (float)(sc & 0xFFu), (d * 0.0625f) * (float)(sc >> 8),
+                       dmin * (float)(mn & 0xFFu), dmin * (float)(mn >> 8)};
 }
 
 template <int XT>
@@ -101,16 +125,6 @@ __device__ __forceinline__ void store_out(void *y, int64_t idx, float v) {
         static_cast<uint16_t *>(y)[idx] = f32_to_bf16_bits(v);
 }
 
-// Per-lane scale state of one weight row in one super-block.
-struct RowScales {
-    float d, dmin;
-    uint32_t s0, s1, s2;
-};
-
-__device__ __forceinline__ RowScales row_scales(u32x4 h) {
-    return RowScales{f16_bits_to_f32(h.x & 0xFFFFu), f16_bits_to_f32(h.x >> 16), h.y, h.z, h.w};
-}
-
 // ---------------------------------------------------------------------------
 // Tiled GEMM.
 //
@@ -120,23 +134,24 @@ __device__ __forceinline__ RowScales row_scales(u32x4 h) {
 // sub-blocks = two MFMA k-steps):
 //   * activations: each stage's TM x 64 tile is copied global -> LDS by the
 //     gfx950 direct-to-LDS loads (buffer_load_dwordx4 ... lds) into a ring
-//     of 4 stage buffers, 3 stages ahead (issued right after the stage
+//     of 5 stage buffers, 4 stages ahead (issued right after the stage
 //     barrier, when every wave has finished reading the buffer being
 //     refilled).  Token t's 16-byte chunk c sits at position c ^ (t & 7) of
-//     the token's 128-byte row, so the fragment reads
-//     (16 tokens x 16 bytes per k-group) hit distinct banks;
-//   * weights: each lane loads the 8 quant bytes of its fragment row three
-//     stages ahead (the block header two stages ahead) and dequantises them
-//     straight into MFMA operand registers, one stage ahead of use: the
+//     the token's 128-byte row, so the fragment reads (16 tokens x 16 bytes
+//     per k-group) hit distinct banks;
+//   * weights: each lane loads the 8 quant bytes of its fragment row four
+//     stages ahead (the block header three stages ahead) and dequantises
+//     them straight into MFMA operand registers, one stage ahead of use: the
 //     dequantisation of stage s+1 (VALU) is written between the MFMAs of
 //     stage s, one (fragment, half) per token fragment, so the two pipes
-//     overlap;
+//     overlap.  The prefetch depth is set by latency: with loads two stages
+//     ahead the kernel waited on memory at every stage;
 //   * per stage: wait until this stage's copies have landed (vmcnt), one
 //     workgroup barrier, refill the freed buffer, then 2 x 4 x TF MFMAs.
 // The vmcnt bound is static: every stage issues the same loads (beyond the
 // last stage they repeat the last stage's addresses into buffers that are
-// never read), so "all but the two most recent stages' loads are done"
-// is the constant kStageLoads*2 (+4 where one of them fetched a header).
+// never read), so the loads issued after stage s's copies are always its
+// own quant bytes, three later stages and one header batch: 3*kXLoads + 20.
 // Split-K (splits > 1): each workgroup covers a range of super-blocks and
 // writes its fp32 tile to a workspace; a second launch (gemm_reduce_kernel)
 // adds the splits in split order and writes the output, so results do not
@@ -145,7 +160,7 @@ __device__ __forceinline__ RowScales row_scales(u32x4 h) {
 constexpr int kGemmWaves = 4;
 constexpr int kRowsPerWave = 64;
 constexpr int kRowsPerWg = kGemmWaves * kRowsPerWave;
-constexpr int kRing = 4;
+constexpr int kRing = 5;
 
 struct GemmParams {
     void *y;
@@ -178,11 +193,38 @@ __device__ __forceinline__ void store4(void *y, int64_t idx, f32x4 v, bool vec_o
     }
 }
 
+// 32x32x16 MFMA (fp32 accumulate) with operands of the x type.  Lane l:
+// src0 = row l%32, 8 k values in slot 8*(l/32); src1 = token l%32, same k
+// slot; dst element i = row 8*(i/4) + 4*(l/32) + i%4 of token l%32.
+template <int XT>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    if (XT == RXQ4_DTYPE_BF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Output position of accumulator element i of (row fragment rf, token
+// fragment tf) held by lane `lane` of wave `wave` in tile (row_tile,
+// tok_tile): rows row..row+3 (j = i/4) of token tok.
+struct OutPos {
+    int row, tok;
+};
+
+template <int TF>
+__device__ __forceinline__ OutPos out_pos(int row_tile, int tok_tile, int wave, int lane, int rf,
+                                          int tf, int j) {
+    return OutPos{row_tile * kRowsPerWg + wave * kRowsPerWave + 32 * rf + 8 * j + 4 * (lane >> 5),
+                  tok_tile * 16 * TF + 32 * tf + (lane & 31)};
+}
+
 template <int XT, int YT, int TF>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
-    constexpr int TM = 16 * TF;
+    static_assert(TF == 8, "the stage body is written for 4 token fragments of 32");
+    constexpr int TM = 16 * TF;                // 128 tokens
+    constexpr int NT = TM / 32;                // 32-token fragments
     constexpr int kXLoads = TM / 32;           // 1 KB direct-to-LDS loads per wave per stage
-    constexpr int kStageLoads = kXLoads + 4;   // + 4 quant-byte loads
     __shared__ __attribute__((aligned(1024))) uint8_t xs[kRing][TM * 128];
 
     const int L = blockIdx.x;
@@ -200,17 +242,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int li = lane & 15;
-    const int g = lane >> 4;
+    const int lr = lane & 31;   // row (A) / token (B) within a 32-fragment
+    const int h = lane >> 5;    // k slot: bytes 16h .. 16h+15 of each 32-byte quant group
     const int K = p.K;
     const int64_t row_bytes = (int64_t)p.nb * kBlockBytes;
     const int row_base = row_tile * kRowsPerWg + wave * kRowsPerWave;
     const int tok_base = tok_tile * TM;
 
-    const uint8_t *wrow[4];
+    const uint8_t *wrow[2];
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
-        wrow[f] = p.w + (int64_t)min(row_base + 16 * f + li, p.M - 1) * row_bytes + sb0 * kBlockBytes;
+    for (int rf = 0; rf < 2; ++rf)
+        wrow[rf] = p.w + (int64_t)min(row_base + 32 * rf + lr, p.M - 1) * row_bytes + sb0 * kBlockBytes;
 
     // Direct-to-LDS copy of stage s (clamped to the last stage), as MUBUF
     // buffer_load_dwordx4 ... lds over the workgroup's token rows (byte
@@ -236,160 +278,214 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
             buffer_to_lds16(xrsrc, &xs[s % kRing][jc * 1024], xoff[i] + k0b);
         }
     };
-    auto load_q = [&](int s, u32x2 *q) {
+    // The lane's 16 quant bytes of stage s for both row fragments.
+    auto load_q = [&](int s, u32x4 *q) {
         const int st = min(s, n_stages - 1);
-        const int off = (st >> 2) * kBlockBytes + 16 + 32 * (st & 3) + 8 * g;
+        const int off = (st >> 2) * kBlockBytes + 16 + 32 * (st & 3) + 16 * h;
 #pragma unroll
-        for (int f = 0; f < 4; ++f) q[f] = *reinterpret_cast<const u32x2 *>(wrow[f] + off);
+        for (int rf = 0; rf < 2; ++rf) q[rf] = load16(wrow[rf] + off);
     };
-    auto load_h = [&](int sbi, u32x4 *h) {
+    auto load_h = [&](int sbi, u32x4 *hd) {
         const int sbc = min(sbi, nsb - 1);
 #pragma unroll
-        for (int f = 0; f < 4; ++f) h[f] = load16(wrow[f] + sbc * kBlockBytes);
+        for (int rf = 0; rf < 2; ++rf) hd[rf] = load16(wrow[rf] + sbc * kBlockBytes);
     };
 
-    f32x4 acc[4][TF];
+    f32x16 acc[2][NT];
 #pragma unroll
-    for (int f = 0; f < 4; ++f)
+    for (int rf = 0; rf < 2; ++rf)
 #pragma unroll
-        for (int t = 0; t < TF; ++t) acc[f][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tf = 0; tf < NT; ++tf) acc[rf][tf] = f32x16{};
 
-    u32x2 q[4][4];      // quant bytes of stages s .. s+3 (ring by s % 4)
-    u32x4 hcur[4], hnext[4];
-    u32x4 a[2][8];      // dequantised operands of stages s (a[s&1]) and s+1: [f] lo, [4+f] hi
+    u32x4 q[4][2];      // quant bytes of stages s .. s+3 (ring by s % 4), per row fragment
+    u32x4 hcur[2], hnext[2];
+    // Dequantised operands of stages s (a[s&1]) and s+1: [rf][k-step]
+    // with k-steps 0: low nibbles of bytes 0-7, 1: low nibbles of bytes
+    // 8-15, 2: high nibbles of bytes 0-7, 3: high nibbles of bytes 8-15 (the
+    // two sub-blocks of the quant group, 8 k each per lane).
+    u32x4 a[2][2][4];
 
-    // Operands of stage st (quant group il of the super-block whose headers
-    // are h) into a[buf].
-    auto dequant_stage = [&](const u32x2 *qs, const u32x4 *h, int il, u32x4 *out) {
+    auto dequant_stage = [&](const u32x4 *qs, const u32x4 *hd, int il, u32x4 (*out)[4]) {
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            const RowScales rs = row_scales(h[f]);
-            uint32_t sc, mn;
-            scale_pair(rs.s0, rs.s1, rs.s2, il, &sc, &mn);
-            out[f] = dequant8<XT>(qs[f].x, qs[f].y, false, rs.d * (float)(sc & 0xFFu),
-                                  rs.dmin * (float)(mn & 0xFFu));
-            out[4 + f] = dequant8<XT>(qs[f].x, qs[f].y, true, rs.d * (float)(sc >> 8),
-                                      rs.dmin * (float)(mn >> 8));
+        for (int rf = 0; rf < 2; ++rf) {
+            const GroupScales g = group_scales(hd[rf], il);
+            out[rf][0] = dequant8<XT>(qs[rf].x, qs[rf].y, false, g.lo, g.dm_lo);
+            out[rf][1] = dequant8<XT>(qs[rf].z, qs[rf].w, false, g.lo, g.dm_lo);
+            out[rf][2] = dequant8<XT>(qs[rf].x, qs[rf].y, true, g.hi, g.dm_hi);
+            out[rf][3] = dequant8<XT>(qs[rf].z, qs[rf].w, true, g.hi, g.dm_hi);
         }
     };
 
-    // Prologue: stages 0..2 in flight, operands of stage 0 ready.
+    // B fragments of token fragment tf of stage st, k-steps as for A: chunk
+    // (16 bytes = 8 k) 2h + step of the low sub-block, 4 + 2h + step of the
+    // high one, from ring buffer st % kRing (chunk c of token t sits at
+    // position c ^ (t & 7)).
+    auto read_b = [&](int st, int tf, u32x4 *b4) {
+        const uint8_t *xb = xs[st % kRing];
+        const int tt = 32 * tf + lr;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int c = (k >> 1) * 4 + 2 * h + (k & 1);
+            b4[k] = *reinterpret_cast<const u32x4 *>(xb + tt * 128 + ((c ^ (tt & 7)) << 4));
+        }
+    };
+    u32x4 bf[2][NT][4];  // B fragments of stages s (bf[s&1]) and s+1
+
+    // Prologue: the loads of stages 0..3 in the order the loop issues them
+    // (stage k's copies, its quant bytes, the header every 4th stage), the
+    // operands of stage 0, then its B fragments once its copies have landed.
+    // (sched_barrier pins the issue order the static vmcnt bounds count on.)
+    constexpr int kQLoads = 2, kHLoads = 2;
     issue_x(0);
+    __builtin_amdgcn_sched_barrier(0);
     load_q(0, q[0]);
     load_h(0, hcur);
     issue_x(1);
+    __builtin_amdgcn_sched_barrier(0);
     load_q(1, q[1]);
     issue_x(2);
+    __builtin_amdgcn_sched_barrier(0);
     load_q(2, q[2]);
+    issue_x(3);
+    __builtin_amdgcn_sched_barrier(0);
+    load_q(3, q[3]);
     dequant_stage(q[0], hcur, 0, a[0]);
+    // loads after stage 0's copies: 4 quant batches, 3 copy batches, 1 header batch
+    wait_vmcnt<3 * kXLoads + 4 * kQLoads + kHLoads>();
+    lds_barrier();
+#pragma unroll
+    for (int tf = 0; tf < NT; ++tf) read_b(0, tf, bf[0][tf]);
 
     for (int sbi = 0; sbi < nsb; ++sbi) {
 #pragma unroll
         for (int il = 0; il < 4; ++il) {
             const int s = 4 * sbi + il;
-            // Copies of stage s have landed once at most the two later
-            // stages' loads are outstanding; then every wave is past stage
-            // s-1, so buffer (s+3) % 4 may be refilled.
-            if (il >= 2)
-                wait_vmcnt<2 * kStageLoads + 4>();
+            // Loads run 4 stages ahead: copies of stage s+4 into ring buffer
+            // (s+4) % 5, quant bytes of stage s+4 into q[il] (it held stage
+            // s, consumed during stage s-1), and at il == 0 the next
+            // super-block's headers.  Stage s's B fragments were read during
+            // stage s-1; this stage reads stage s+1's, so it waits for the
+            // copies of stage s+1: the loads issued after them are its quant
+            // bytes, two later stages and, unless il == 0, one header batch.
+            // After the barrier every wave has its stage s+1 copies and is
+            // past stage s-1, whose buffer is refilled.
+            if (il == 0)
+                wait_vmcnt<2 * kXLoads + 3 * kQLoads>();
             else
-                wait_vmcnt<2 * kStageLoads>();
+                wait_vmcnt<2 * kXLoads + 3 * kQLoads + kHLoads>();
             lds_barrier();
-            issue_x(s + 3);
-            load_q(s + 3, q[(il + 3) & 3]);
-            if (il == 1) load_h(sbi + 1, hnext);
+            issue_x(s + 4);
+            __builtin_amdgcn_sched_barrier(0);
+            load_q(s + 4, q[il]);
+            if (il == 0) load_h(sbi + 1, hnext);
 
-            // MFMAs of stage s interleaved with the dequantisation of stage
-            // s+1 (the next quant group, or group 0 of the next super-block).
-            const u32x4 *acur = a[il & 1];
-            u32x4 *anext = a[(il + 1) & 1];
+            // 32 MFMAs of stage s (k-step major: 8 independent accumulators
+            // between dependent ones) interleaved with the dequantisation
+            // of stage s+1 (the next quant group, or group 0 of the next
+            // super-block), one 8-weight operand per 4 MFMAs, and with the
+            // reads of stage s+1's B fragments.  sched_barrier keeps the
+            // order, so VALU and LDS work issue while the matrix core runs.
+            u32x4 (*acur)[4] = a[il & 1];
+            u32x4 (*anext)[4] = a[(il + 1) & 1];
             const u32x4 *hn = il == 3 ? hnext : hcur;
-            const u32x2 *qn = q[(il + 1) & 3];
-            const uint8_t *xb = xs[s % kRing];
+            const u32x4 *qn = q[(il + 1) & 3];
+            GroupScales gs[2];  // scales of stage s+1
 #pragma unroll
-            for (int t = 0; t < TF; ++t) {
-                const int tt = 16 * t + li;
-                const u32x4 b_lo =
-                    *reinterpret_cast<const u32x4 *>(xb + tt * 128 + (((g) ^ (tt & 7)) << 4));
-                const u32x4 b_hi =
-                    *reinterpret_cast<const u32x4 *>(xb + tt * 128 + (((4 + g) ^ (tt & 7)) << 4));
+            for (int rf = 0; rf < 2; ++rf) gs[rf] = group_scales(hn[rf], (il + 1) & 3);
+            u32x4 (*bc)[4] = bf[il & 1];
+            u32x4 (*bn)[4] = bf[(il + 1) & 1];
 #pragma unroll
-                for (int f = 0; f < 4; ++f) {
-                    acc[f][t] = mfma<XT>(acur[f], b_lo, acc[f][t]);
-                    acc[f][t] = mfma<XT>(acur[4 + f], b_hi, acc[f][t]);
-                }
-                if (TF == 8) {
-                    // one (fragment, half) of the next stage per token fragment
-                    const int f = t >> 1;
-                    const RowScales rs = row_scales(hn[f]);
-                    uint32_t sc, mn;
-                    scale_pair(rs.s0, rs.s1, rs.s2, (il + 1) & 3, &sc, &mn);
-                    if ((t & 1) == 0)
-                        anext[f] = dequant8<XT>(qn[f].x, qn[f].y, false, rs.d * (float)(sc & 0xFFu),
-                                                rs.dmin * (float)(mn & 0xFFu));
-                    else
-                        anext[4 + f] = dequant8<XT>(qn[f].x, qn[f].y, true, rs.d * (float)(sc >> 8),
-                                                    rs.dmin * (float)(mn >> 8));
+            for (int k = 0; k < 4; ++k) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    // 4 MFMAs: token fragments 2*half, 2*half+1 x row fragments
+#pragma unroll
+                    for (int tf = 2 * half; tf < 2 * half + 2; ++tf)
+#pragma unroll
+                        for (int rf = 0; rf < 2; ++rf)
+                            acc[rf][tf] = mfma32<XT>(acur[rf][k], bc[tf][k], acc[rf][tf]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    // operand (rf = half, k-step k) of stage s+1
+                    const int rf = half;
+                    const bool hi = k >= 2;
+                    const uint32_t v0 = (k & 1) ? qn[rf].z : qn[rf].x;
+                    const uint32_t v1 = (k & 1) ? qn[rf].w : qn[rf].y;
+                    anext[rf][k] = dequant8<XT>(v0, v1, hi, hi ? gs[rf].hi : gs[rf].lo,
+                                                hi ? gs[rf].dm_hi : gs[rf].dm_lo);
+                    // B fragments of stage s+1: token fragment k, k-steps 2*half, 2*half+1
+#pragma unroll
+                    for (int kk = 2 * half; kk < 2 * half + 2; ++kk) {
+                        const uint8_t *xb = xs[(s + 1) % kRing];
+                        const int tt = 32 * k + lr;
+                        const int c = (kk >> 1) * 4 + 2 * h + (kk & 1);
+                        bn[k][kk] = *reinterpret_cast<const u32x4 *>(xb + tt * 128 + ((c ^ (tt & 7)) << 4));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if (TF != 8) dequant_stage(qn, hn, (il + 1) & 3, anext);
             if (il == 3) {
 #pragma unroll
-                for (int f = 0; f < 4; ++f) hcur[f] = hnext[f];
+                for (int rf = 0; rf < 2; ++rf) hcur[rf] = hnext[rf];
             }
         }
     }
     wait_vmcnt<0>();  // trailing clamped copies must land before the workgroup exits
 
     if (p.splits > 1) {
+        // partial tile: per thread 2 x NT x 4 float4 in (rf, tf, j) order
         f32x4 *part = reinterpret_cast<f32x4 *>(p.ws) +
-                      ((int64_t)(tile * p.splits + split) * (4 * TF)) * 256 + tid;
+                      ((int64_t)(tile * p.splits + split) * (8 * NT)) * 256 + tid;
 #pragma unroll
-        for (int f = 0; f < 4; ++f)
+        for (int rf = 0; rf < 2; ++rf)
 #pragma unroll
-            for (int t = 0; t < TF; ++t) part[(f * TF + t) * 256] = acc[f][t];
+            for (int tf = 0; tf < NT; ++tf)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    part[((rf * NT + tf) * 4 + j) * 256] =
+                        f32x4{acc[rf][tf][4 * j], acc[rf][tf][4 * j + 1], acc[rf][tf][4 * j + 2],
+                              acc[rf][tf][4 * j + 3]};
         return;
     }
     const bool vec_ok = (p.M & 3) == 0;
-    // lane holds rows row_base + 16f + 4g + r of token tok_base + 16t + li
 #pragma unroll
-    for (int t = 0; t < TF; ++t) {
-        const int tok = tok_base + 16 * t + li;
-        if (tok >= p.N) continue;
+    for (int rf = 0; rf < 2; ++rf)
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            const int row = row_base + 16 * f + 4 * g;
-            if (row >= p.M) continue;
-            const int valid = min(4, p.M - row);
-            store4<YT>(p.y, (int64_t)tok * p.M + row, acc[f][t], vec_ok && valid == 4, valid);
-        }
-    }
+        for (int tf = 0; tf < NT; ++tf)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const OutPos o = out_pos<TF>(row_tile, tok_tile, wave, lane, rf, tf, j);
+                if (o.tok >= p.N || o.row >= p.M) continue;
+                const int valid = min(4, p.M - o.row);
+                store4<YT>(p.y, (int64_t)o.tok * p.M + o.row,
+                           f32x4{acc[rf][tf][4 * j], acc[rf][tf][4 * j + 1], acc[rf][tf][4 * j + 2],
+                                 acc[rf][tf][4 * j + 3]},
+                           vec_ok && valid == 4, valid);
+            }
 }
 
-// Split-K reduction: block (tile, f*TF+t) sums the splits of one fragment
-// set of the tile in split order; thread tid holds the same element positions
-// as thread tid of the GEMM workgroups.
+// Split-K reduction: block (tile, e) with e = (rf*NT + tf)*4 + j sums the
+// splits of one float4 of every thread of the tile in split order; thread
+// tid holds the positions of thread tid of the GEMM workgroups.
 template <int YT, int TF>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
-    constexpr int TM = 16 * TF;
+    constexpr int NT = TF / 2;
+    constexpr int E = 8 * NT;  // float4 per thread
     const int tid = threadIdx.x;
-    const int tile = blockIdx.x / (4 * TF);
-    const int ft = blockIdx.x % (4 * TF);
-    const int f = ft / TF, t = ft % TF;
+    const int tile = blockIdx.x / E;
+    const int e = blockIdx.x % E;
+    const int rf = e / (4 * NT), tf = (e / 4) % NT, j = e % 4;
     const int row_tile = tile / p.tok_tiles, tok_tile = tile % p.tok_tiles;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int tok = tok_tile * TM + 16 * t + (lane & 15);
-    const int row = row_tile * kRowsPerWg + wave * kRowsPerWave + 16 * f + 4 * (lane >> 4);
+    const OutPos o = out_pos<TF>(row_tile, tok_tile, tid >> 6, tid & 63, rf, tf, j);
     const f32x4 *src = reinterpret_cast<const f32x4 *>(p.ws) +
-                       ((int64_t)tile * p.splits * (4 * TF) + ft) * 256 + tid;
+                       ((int64_t)tile * p.splits * E + e) * 256 + tid;
     f32x4 sum = src[0];
     for (int sp = 1; sp < p.splits; ++sp) {
-        const f32x4 v = src[(int64_t)sp * (4 * TF) * 256];
+        const f32x4 v = src[(int64_t)sp * E * 256];
         sum = f32x4{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
     }
-    if (tok >= p.N || row >= p.M) return;
-    const int valid = min(4, p.M - row);
-    store4<YT>(p.y, (int64_t)tok * p.M + row, sum, (p.M & 3) == 0 && valid == 4, valid);
+    if (o.tok >= p.N || o.row >= p.M) return;
+    const int valid = min(4, p.M - o.row);
+    store4<YT>(p.y, (int64_t)o.tok * p.M + o.row, sum, (p.M & 3) == 0 && valid == 4, valid);
 }
 
 // ---------------------------------------------------------------------------
@@ -418,7 +514,7 @@ __global__ __launch_bounds__(256) void gemv_tokens_kernel(void *__restrict__ y,
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int sb = wave; sb < nb; sb += 4) {
         const uint8_t *blk = wr + sb * kBlockBytes;
-        const RowScales rs = row_scales(load16(blk));
+        const u32x4 hdr = load16(blk);
         u32x2 q[4];
         u32x4 b[8];
 #pragma unroll
@@ -430,12 +526,9 @@ __global__ __launch_bounds__(256) void gemv_tokens_kernel(void *__restrict__ y,
         }
 #pragma unroll
         for (int il = 0; il < 4; ++il) {
-            uint32_t sc, mn;
-            scale_pair(rs.s0, rs.s1, rs.s2, il, &sc, &mn);
-            const u32x4 a_lo = dequant8<XT>(q[il].x, q[il].y, false, rs.d * (float)(sc & 0xFFu),
-                                            rs.dmin * (float)(mn & 0xFFu));
-            const u32x4 a_hi = dequant8<XT>(q[il].x, q[il].y, true, rs.d * (float)(sc >> 8),
-                                            rs.dmin * (float)(mn >> 8));
+            const GroupScales gsc = group_scales(hdr, il);
+            const u32x4 a_lo = dequant8<XT>(q[il].x, q[il].y, false, gsc.lo, gsc.dm_lo);
+            const u32x4 a_hi = dequant8<XT>(q[il].x, q[il].y, true, gsc.hi, gsc.dm_hi);
             acc = mfma<XT>(a_lo, b[2 * il], acc);
             acc = mfma<XT>(a_hi, b[2 * il + 1], acc);
         }
@@ -533,7 +626,7 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     p.total_units = tiles * splits;
     p.units_per_xcd = (p.total_units + 7) / 8;
     gemm_kernel<XT, YT, TF><<<8 * p.units_per_xcd, 256, 0, st>>>(p);
-    if (splits > 1) gemm_reduce_kernel<YT, TF><<<tiles * 4 * TF, 256, 0, st>>>(p);
+    if (splits > 1) gemm_reduce_kernel<YT, TF><<<tiles * 4 * TF, 256, 0, st>>>(p);  // 4*TF = 8*NT float4 per thread
     return hipGetLastError();
 }
 
