@@ -374,17 +374,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
             else
                 wait_vmcnt<2 * kXLoads + 3 * kQLoads + kHLoads>();
             lds_barrier();
+            // The previous stage's reads of this stage's B fragments are
+            // long done; saying so up front keeps the compiler from waiting
+            // inside the MFMA stream on LDS reads issued in this stage (the
+            // LDS counter completes in order).
+            wait_lgkmcnt0();
             issue_x(s + 4);
             __builtin_amdgcn_sched_barrier(0);
             load_q(s + 4, q[il]);
             if (il == 0) load_h(sbi + 1, hnext);
 
             // 32 MFMAs of stage s (k-step major: 8 independent accumulators
-            // between dependent ones) interleaved with the dequantisation
-            // of stage s+1 (the next quant group, or group 0 of the next
-            // super-block), one 8-weight operand per 4 MFMAs, and with the
-            // reads of stage s+1's B fragments.  sched_barrier keeps the
-            // order, so VALU and LDS work issue while the matrix core runs.
+            // between dependent ones), each followed by a quarter of one
+            // 8-weight operand of stage s+1 (the next quant group, or group 0
+            // of the next super-block; ~5 VALU ops) and, every other MFMA, one
+            // read of stage s+1's B fragments.  A wave issues in order, so
+            // this one-to-one pattern is what lets the VALU and LDS work run
+            // while the matrix core works on the preceding MFMA (32 cycles);
+            // sched_barrier keeps the order.
             u32x4 (*acur)[4] = a[il & 1];
             u32x4 (*anext)[4] = a[(il + 1) & 1];
             const u32x4 *hn = il == 3 ? hnext : hcur;
@@ -394,34 +401,39 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
             for (int rf = 0; rf < 2; ++rf) gs[rf] = group_scales(hn[rf], (il + 1) & 3);
             u32x4 (*bc)[4] = bf[il & 1];
             u32x4 (*bn)[4] = bf[(il + 1) & 1];
+            const uint8_t *xnb = xs[(s + 1) % kRing];
+            uint32_t m0 = 0, m1 = 0, o0 = 0, o1 = 0, o2 = 0, o3 = 0;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    // 4 MFMAs: token fragments 2*half, 2*half+1 x row fragments
-#pragma unroll
-                    for (int tf = 2 * half; tf < 2 * half + 2; ++tf)
-#pragma unroll
-                        for (int rf = 0; rf < 2; ++rf)
-                            acc[rf][tf] = mfma32<XT>(acur[rf][k], bc[tf][k], acc[rf][tf]);
-                    __builtin_amdgcn_sched_barrier(0);
-                    // operand (rf = half, k-step k) of stage s+1
-                    const int rf = half;
-                    const bool hi = k >= 2;
-                    const uint32_t v0 = (k & 1) ? qn[rf].z : qn[rf].x;
-                    const uint32_t v1 = (k & 1) ? qn[rf].w : qn[rf].y;
-                    anext[rf][k] = dequant8<XT>(v0, v1, hi, hi ? gs[rf].hi : gs[rf].lo,
-                                                hi ? gs[rf].dm_hi : gs[rf].dm_lo);
-                    // B fragments of stage s+1: token fragment k, k-steps 2*half, 2*half+1
-#pragma unroll
-                    for (int kk = 2 * half; kk < 2 * half + 2; ++kk) {
-                        const uint8_t *xb = xs[(s + 1) % kRing];
-                        const int tt = 32 * k + lr;
-                        const int c = (kk >> 1) * 4 + 2 * h + (kk & 1);
-                        bn[k][kk] = *reinterpret_cast<const u32x4 *>(xb + tt * 128 + ((c ^ (tt & 7)) << 4));
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
+            for (int idx = 0; idx < 32; ++idx) {
+                const int k = idx >> 3, tf = (idx >> 1) & 3, rf = idx & 1;
+                acc[rf][tf] = mfma32<XT>(acur[rf][k], bc[tf][k], acc[rf][tf]);
+                __builtin_amdgcn_sched_barrier(0);
+                // operand op = (rf2, k2) of stage s+1, piece idx % 4
+                const int op = idx >> 2, rf2 = op >> 2, k2 = op & 3, piece = idx & 3;
+                const bool hi = k2 >= 2;
+                const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+                const float sc = hi ? gs[rf2].hi : gs[rf2].lo;
+                const float dm = hi ? gs[rf2].dm_hi : gs[rf2].dm_lo;
+                if (piece == 0) {
+                    m0 = mask_opaque((k2 & 1) ? qn[rf2].z : qn[rf2].x, mask);
+                    o0 = dq_pair<XT>(m0, 0, sc, dm);
+                } else if (piece == 1) {
+                    o1 = dq_pair<XT>(m0, 2, sc, dm);
+                } else if (piece == 2) {
+                    m1 = mask_opaque((k2 & 1) ? qn[rf2].w : qn[rf2].y, mask);
+                    o2 = dq_pair<XT>(m1, 0, sc, dm);
+                } else {
+                    o3 = dq_pair<XT>(m1, 2, sc, dm);
+                    anext[rf2][k2] = u32x4{o0, o1, o2, o3};
                 }
+                if ((idx & 1) == 0) {
+                    // B fragment r = idx / 2 of stage s+1: token fragment r / 4, k-step r % 4
+                    const int r = idx >> 1, tf2 = r >> 2, kk = r & 3;
+                    const int tt = 32 * tf2 + lr;
+                    const int c = (kk >> 1) * 4 + 2 * h + (kk & 1);
+                    bn[tf2][kk] = *reinterpret_cast<const u32x4 *>(xnb + tt * 128 + ((c ^ (tt & 7)) << 4));
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
             if (il == 3) {
 #pragma unroll

@@ -104,6 +104,11 @@ __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rsrc, voi
         rsrc, (void __attribute__((address_space(3))) *)lds, 16, voffset, 0, 0, 0);
 }
 
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt untouched).
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
+}
+
 // s_waitcnt vmcnt(N) (lgkmcnt and expcnt untouched).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
