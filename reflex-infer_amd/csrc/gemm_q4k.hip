@@ -48,52 +48,43 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
 }
 
-// v & mask as an opaque value, so that the byte extracts below stay
-// v_cvt_f32_ubyte{0..3} instead of being folded into bit-field extracts.
-__device__ __forceinline__ uint32_t mask_opaque(uint32_t v, uint32_t mask) {
-    uint32_t r;
-    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(mask), "v"(v));
-    return r;
+// Two fp32 values from bytes 2*word, 2*word+1 of m.  Each byte is a nibble
+// value q in [0, 15]; read as an FP8 E4M3 (OCP) pattern it is exactly
+// q * 2^-9 (subnormal for q < 8), so v_cvt_pk_f32_fp8 turns two nibbles
+// into exact floats with one instruction.
+template <bool WORD>
+__device__ __forceinline__ f32x2 nibbles_f32(uint32_t m) {
+    return __builtin_amdgcn_cvt_pk_f32_fp8((int)m, WORD);
 }
 
-// Four weights from the four bytes of m (each a nibble value, or 16 x a
-// nibble value when `scale` carries the factor 1/16): w = scale*b - dm.
-// The products are exact, so each w has the single fp32 rounding of the
-// reference formula d*sc*q - dmin*m.
+// Four weights from the four nibble bytes of m: w = scale512 * (q * 2^-9)
+// - dm with scale512 = d*sc*512, i.e. d*sc*q - dmin*m with the single fp32
+// rounding of the reference (the product is exact), then RNE to the operand
+// type.
 template <int XT>
-__device__ __forceinline__ void dequant4(uint32_t m, float scale, float dm, uint32_t *out) {
-    const float w0 = scale * (float)(m & 0xFFu) - dm;
-    const float w1 = scale * (float)((m >> 8) & 0xFFu) - dm;
-    const float w2 = scale * (float)((m >> 16) & 0xFFu) - dm;
-    const float w3 = scale * (float)(m >> 24) - dm;
-    out[0] = pack2<XT>(w0, w1);
-    out[1] = pack2<XT>(w2, w3);
+__device__ __forceinline__ void dequant4(uint32_t m, float scale512, float dm, uint32_t *out) {
+    const f32x2 f01 = nibbles_f32<false>(m), f23 = nibbles_f32<true>(m);
+    out[0] = pack2<XT>(scale512 * f01[0] - dm, scale512 * f01[1] - dm);
+    out[1] = pack2<XT>(scale512 * f23[0] - dm, scale512 * f23[1] - dm);
 }
 
-// Two weights from bytes b, b+1 of m (nibble values, or 16 x nibble values
-// with scale = d*sc/16), packed: w = scale*byte - dm, one fp32 rounding.
-template <int XT>
-__device__ __forceinline__ uint32_t dq_pair(uint32_t m, int b, float scale, float dm) {
-    const float w0 = scale * (float)((m >> (8 * b)) & 0xFFu) - dm;
-    const float w1 = scale * (float)((m >> (8 * b + 8)) & 0xFFu) - dm;
-    return pack2<XT>(w0, w1);
+// Nibble bytes of v: low nibbles (hi = false) or high nibbles.
+__device__ __forceinline__ uint32_t nibble_bytes(uint32_t v, bool hi) {
+    return (hi ? (v >> 4) : v) & 0x0F0F0F0Fu;
 }
 
 // Eight weights from the low (hi = false) or high nibbles of bytes v0, v1.
-// High nibbles are used in place (16*q): the caller passes scale = d*sc/16
-// for them, an exact rescaling.
 template <int XT>
-__device__ __forceinline__ u32x4 dequant8(uint32_t v0, uint32_t v1, bool hi, float scale,
+__device__ __forceinline__ u32x4 dequant8(uint32_t v0, uint32_t v1, bool hi, float scale512,
                                           float dm) {
-    const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
     uint32_t o[4];
-    dequant4<XT>(mask_opaque(v0, mask), scale, dm, o);
-    dequant4<XT>(mask_opaque(v1, mask), scale, dm, o + 2);
+    dequant4<XT>(nibble_bytes(v0, hi), scale512, dm, o);
+    dequant4<XT>(nibble_bytes(v1, hi), scale512, dm, o + 2);
     return u32x4{o[0], o[1], o[2], o[3]};
 }
 
 // Scales of one weight row for quant group il: sub-block 2il (low nibbles)
-// and 2il+1 (high nibbles, scale pre-divided by 16).
+// and 2il+1 (high nibbles), each times 512 for dequant4.
 struct GroupScales {
     float lo, hi, dm_lo, dm_hi;
 };
@@ -102,7 +93,8 @@ __device__ __forceinline__ GroupScales group_scales(u32x4 h, int il) {
     const float d = f16_bits_to_f32(h.x & 0xFFFFu), dmin = f16_bits_to_f32(h.x >> 16);
     uint32_t sc, mn;
     scale_pair(h.y, h.z, h.w, il, &sc, &mn);
-    return GroupScales{d * (float)(sc & 0xFFu), (d * 0.0625f) * (float)(sc >> 8),
+    const float d512 = d * 512.0f;
+    return GroupScales{d512 * (float)(sc & 0xFFu), d512 * (float)(sc >> 8),
                        dmin * (float)(mn & 0xFFu), dmin * (float)(mn >> 8)};
 }
 
@@ -411,19 +403,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
                 // operand op = (rf2, k2) of stage s+1, piece idx % 4
                 const int op = idx >> 2, rf2 = op >> 2, k2 = op & 3, piece = idx & 3;
                 const bool hi = k2 >= 2;
-                const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
                 const float sc = hi ? gs[rf2].hi : gs[rf2].lo;
                 const float dm = hi ? gs[rf2].dm_hi : gs[rf2].dm_lo;
                 if (piece == 0) {
-                    m0 = mask_opaque((k2 & 1) ? qn[rf2].z : qn[rf2].x, mask);
-                    o0 = dq_pair<XT>(m0, 0, sc, dm);
+                    m0 = nibble_bytes((k2 & 1) ? qn[rf2].z : qn[rf2].x, hi);
+                    const f32x2 f = nibbles_f32<false>(m0);
+                    o0 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
                 } else if (piece == 1) {
-                    o1 = dq_pair<XT>(m0, 2, sc, dm);
+                    const f32x2 f = nibbles_f32<true>(m0);
+                    o1 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
                 } else if (piece == 2) {
-                    m1 = mask_opaque((k2 & 1) ? qn[rf2].w : qn[rf2].y, mask);
-                    o2 = dq_pair<XT>(m1, 0, sc, dm);
+                    m1 = nibble_bytes((k2 & 1) ? qn[rf2].w : qn[rf2].y, hi);
+                    const f32x2 f = nibbles_f32<false>(m1);
+                    o2 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
                 } else {
-                    o3 = dq_pair<XT>(m1, 2, sc, dm);
+                    const f32x2 f = nibbles_f32<true>(m1);
+                    o3 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
                     anext[rf2][k2] = u32x4{o0, o1, o2, o3};
                 }
                 if ((idx & 1) == 0) {
