@@ -21,6 +21,9 @@ stream and timed with HIP events recorded on that stream around replays:
   per_kernel   every decode projection, the LM head [151936 x 2048] fp32
                GEMV, the 4096-id Zipf(1.1) embedding gather, and the prefill
                GEMM at m=512 (TFLOP/s, BASELINE metric's second half)
+  small_batch_decode  m in {1,2,4,8,16} tokens on gate+up and down
+               (where weight reuse ends the purely
+               bandwidth-bound regime)
   cpu_baseline the oracle's restatement of the reference CPU GEMV
                (gemv_quant_cpu) over the full 36-layer set, single thread.
 """
@@ -332,6 +335,23 @@ def main() -> int:
         kernels["embed_gather_4096_zipf"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
                                              "unique_rows": uniq}
         del heads
+
+        # Small-batch decode: m tokens through
+        # gemm_quant_batched's C-ABI form with fp16 x / y on the decode
+        # set's gate+up and down weights (distinct layers per launch).
+        small = {}
+        for name, key, M, K in (("gate_up", "gu", 2 * FFN, HIDDEN), ("down", "down", HIDDEN, FFN)):
+            for m in (1, 2, 4, 8, 16):
+                xs_m = gen(50_000 + m + K, (m, K), 1.0).half()
+                ys_m = torch.empty((m, M), dtype=torch.float16, device=dev)
+
+                def sb_launch(i, xs_m=xs_m, ys_m=ys_m, key=key, M=M, K=K, m=m):
+                    capi.gemm_f16(ys_m, layers[i % N_LAYERS][key], xs_m, M, m, K, stream=sp)
+                med, _ = per_launch(sb_launch, N_LAYERS)
+                b = qbytes(M, K) + m * K * 2 + m * M * 2
+                small[f"{name}_{M}x{K}_m{m}"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
+                                                 "GFLOPs": round(2 * m * M * K / med / 1e3, 1)}
+        extras["small_batch_decode"] = small
 
         # Prefill GEMM at m = 512 (bf16 activations, bf16 out).
         for (M, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):

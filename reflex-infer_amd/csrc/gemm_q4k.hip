@@ -496,64 +496,104 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Small batch (2..16 tokens): one 16-row x 16-token output fragment per
-// workgroup, the K super-blocks split over 4 waves, x fragments read straight
-// from global memory (the whole x is a few KB and stays in L2), partial sums
-// added in wave order through LDS.
-template <int XT, int YT>
-__global__ __launch_bounds__(256) void gemv_tokens_kernel(void *__restrict__ y,
-                                                          const uint8_t *__restrict__ w,
-                                                          const uint16_t *__restrict__ x, int M,
-                                                          int N, int K) {
-    __shared__ f32x4 part[4][64];
+// Small batch (2..16 tokens): a workgroup of KW waves owns 16*RT weight rows
+// x 16 tokens.  The K super-blocks are dealt to the waves round-robin (wave
+// w: w, w+KW, ...); each wave computes RT 16x16 fragments with
+// v_mfma_f32_16x16x32 (A = 16 weight rows, B = the 16 tokens), so one x
+// fragment serves RT row tiles.  Each wave keeps two super-blocks of weights
+// and x in flight (loads unconditional, clamped to the last super-block, so
+// the compiler's vmcnt waits stay exact).  x is read through a buffer
+// resource bounded at N*K elements: the lanes of tokens >= N read past it and
+// get zeros without touching memory.  Partial sums are added in wave order
+// through LDS.
+template <int XT, int YT, int RT, int KW>
+__global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
+    void *__restrict__ y, const uint8_t *__restrict__ w, const uint16_t *__restrict__ x, int M,
+    int N, int K) {
+    __shared__ f32x4 part[KW][RT][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15;
     const int g = lane >> 4;
     const int nb = K >> 8;
-    const int row0 = blockIdx.x * 16;
+    const int row0 = blockIdx.x * 16 * RT;
     const int64_t row_bytes = (int64_t)nb * kBlockBytes;
-    const uint8_t *wr = w + min(row0 + li, M - 1) * row_bytes;
-    const bool tok_ok = li < N;
-    const uint16_t *xt = x + (int64_t)(tok_ok ? li : 0) * K;
+    const uint8_t *wr[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) wr[t] = w + min(row0 + 16 * t + li, M - 1) * row_bytes;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, N * K * 2);
+    const int xoff = li * K * 2 + 16 * g;  // bytes; >= N*K*2 for tokens >= N
+    const int n_w = wave < nb ? (nb - 1 - wave) / KW + 1 : 0;  // super-blocks of this wave
 
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int sb = wave; sb < nb; sb += 4) {
-        const uint8_t *blk = wr + sb * kBlockBytes;
-        const u32x4 hdr = load16(blk);
-        u32x2 q[4];
+    struct Sb {
+        u32x4 hdr[RT];
+        u32x2 q[RT][4];
         u32x4 b[8];
+    };
+    auto load = [&](int i, Sb &o) {
+        const int sb = min(wave + i * KW, nb - 1);
 #pragma unroll
-        for (int il = 0; il < 4; ++il) {
-            q[il] = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * il + 8 * g);
-            const int k0 = sb * 256 + 64 * il + 8 * g;
-            b[2 * il] = tok_ok ? load16(xt + k0) : u32x4{0, 0, 0, 0};
-            b[2 * il + 1] = tok_ok ? load16(xt + k0 + 32) : u32x4{0, 0, 0, 0};
+        for (int t = 0; t < RT; ++t) {
+            const uint8_t *blk = wr[t] + sb * kBlockBytes;
+            o.hdr[t] = load16(blk);
+#pragma unroll
+            for (int il = 0; il < 4; ++il)
+                o.q[t][il] = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * il + 8 * g);
         }
 #pragma unroll
         for (int il = 0; il < 4; ++il) {
-            const GroupScales gsc = group_scales(hdr, il);
-            const u32x4 a_lo = dequant8<XT>(q[il].x, q[il].y, false, gsc.lo, gsc.dm_lo);
-            const u32x4 a_hi = dequant8<XT>(q[il].x, q[il].y, true, gsc.hi, gsc.dm_hi);
-            acc = mfma<XT>(a_lo, b[2 * il], acc);
-            acc = mfma<XT>(a_hi, b[2 * il + 1], acc);
+            const int off = xoff + 2 * (sb * 256 + 64 * il);
+            o.b[2 * il] = buffer_load16(xr, off);
+            o.b[2 * il + 1] = buffer_load16(xr, off + 64);
         }
+    };
+    f32x4 acc[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Sb &o) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int il = 0; il < 4; ++il) {
+                const GroupScales gsc = group_scales(o.hdr[t], il);
+                const u32x4 a_lo =
+                    dequant8<XT>(o.q[t][il].x, o.q[t][il].y, false, gsc.lo, gsc.dm_lo);
+                const u32x4 a_hi =
+                    dequant8<XT>(o.q[t][il].x, o.q[t][il].y, true, gsc.hi, gsc.dm_hi);
+                acc[t] = mfma<XT>(a_lo, o.b[2 * il], acc[t]);
+                acc[t] = mfma<XT>(a_hi, o.b[2 * il + 1], acc[t]);
+            }
+        }
+    };
+    Sb A, B;
+    load(0, A);
+    load(1, B);
+    int i = 0;
+    for (; i + 2 < n_w; i += 2) {
+        compute(A);
+        load(i + 2, A);
+        compute(B);
+        load(i + 3, B);
     }
-    part[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
-        f32x4 s = part[0][lane];
+    if (i < n_w) compute(A);
+    if (i + 1 < n_w) compute(B);
+
 #pragma unroll
-        for (int j = 1; j < 4; ++j) {
-            const f32x4 o = part[j][lane];
-            s = f32x4{s[0] + o[0], s[1] + o[1], s[2] + o[2], s[3] + o[3]};
+    for (int t = 0; t < RT; ++t) part[wave][t][lane] = acc[t];
+    __syncthreads();
+    for (int t = wave; t < RT; t += KW) {
+        f32x4 sum = part[0][t][lane];
+#pragma unroll
+        for (int j = 1; j < KW; ++j) {
+            const f32x4 o = part[j][t][lane];
+            sum = f32x4{sum[0] + o[0], sum[1] + o[1], sum[2] + o[2], sum[3] + o[3]};
         }
-        if (tok_ok) {
+        if (li < N) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = row0 + 4 * g + r;
-                if (row < M) store_out<YT>(y, (int64_t)li * M + row, s[r]);
+                const int row = row0 + 16 * t + 4 * g + r;
+                if (row < M) store_out<YT>(y, (int64_t)li * M + row, sum[r]);
             }
         }
     }
@@ -650,20 +690,36 @@ hipError_t launch_gemm(void *y, int y_dtype, const uint8_t *w, const void *x, in
     return launch_gemm_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
 }
 
+template <int XT, int YT>
+static void launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, int M, int n_tok,
+                            int K, hipStream_t st) {
+    // Four waves split K.  Two row tiles per wave halve the x traffic per
+    // weight byte and pay off once there are enough of them to give about
+    // four waves per CU (1024 waves); a measured sweep of 1/2/4 row tiles and
+    // 1/2/4/8 waves on gate+up [22016 x 2048], down [2048 x 11008] and QKV
+    // [2560 x 2048] at 2..16 tokens put these two shapes first.
+    constexpr int kWaves = 4;
+    const int t2 = (M + 31) / 32;
+    if (t2 * kWaves >= 1024)
+        gemv_tokens_kernel<XT, YT, 2, kWaves><<<t2, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+    else
+        gemv_tokens_kernel<XT, YT, 1, kWaves>
+            <<<(M + 15) / 16, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+}
+
 hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void *x,
                               int x_dtype, int M, int n_tok, int K, hipStream_t st) {
     const uint16_t *xx = static_cast<const uint16_t *>(x);
-    const int grid = (M + 15) / 16;
     if (x_dtype == RXQ4_DTYPE_BF16) {
         if (y_dtype == RXQ4_DTYPE_BF16)
-            gemv_tokens_kernel<RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16><<<grid, 256, 0, st>>>(y, w, xx, M, n_tok, K);
+            launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, n_tok, K, st);
         else
-            gemv_tokens_kernel<RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32><<<grid, 256, 0, st>>>(y, w, xx, M, n_tok, K);
+            launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
     } else {
         if (y_dtype == RXQ4_DTYPE_F16)
-            gemv_tokens_kernel<RXQ4_DTYPE_F16, RXQ4_DTYPE_F16><<<grid, 256, 0, st>>>(y, w, xx, M, n_tok, K);
+            launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, n_tok, K, st);
         else
-            gemv_tokens_kernel<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32><<<grid, 256, 0, st>>>(y, w, xx, M, n_tok, K);
+            launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
     }
     return hipGetLastError();
 }

@@ -97,6 +97,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, in
                                              0x00020000);
 }
 
+// 16 bytes per lane from rsrc + voffset into registers (zeros past the end).
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int voffset) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, 0, 0);
+}
+
 // 16 bytes per lane, global (rsrc + voffset) -> LDS at lds + 16 * lane.
 __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds,
                                                 int voffset) {
