@@ -52,6 +52,11 @@ def lib() -> ctypes.CDLL:
             "orc_gemv_f64": (None, [P, P, I64, I, P]),
             "orc_gemm_f64": (None, [P, P, I64, I64, I, I, P]),
             "orc_quantize_rows": (None, [P, I64, I, P]),
+            "orc_block_bytes": (I, [I]),
+            "orc_kq_dequant_rows_f32": (None, [P, I, I64, I64, I, P]),
+            "orc_kq_embed_rows_f16": (None, [P, I, I64, I, P, I64, P]),
+            "orc_kq_gemv_f32": (None, [P, I, P, I64, I64, I, P]),
+            "orc_kq_gemm_f64": (None, [P, I, P, I64, I64, I, I, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -208,6 +213,54 @@ def quantize(src: np.ndarray) -> np.ndarray:
     out = np.empty((rows, (K // QK_K) * BLOCK_BYTES), dtype=np.uint8)
     lib().orc_quantize_rows(_p(src), rows, K, _p(out))
     return out
+
+
+# ---------------------------------------------------------------- Q5_K / Q6_K
+TYPE_BYTES = {12: 144, 13: 176, 14: 210}
+
+
+def _wt(W, K, t):
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    assert W.size % ((K // QK_K) * TYPE_BYTES[t]) == 0
+    return W, W.size // ((K // QK_K) * TYPE_BYTES[t])
+
+
+def kq_dequant_f32(W, K, t, row0=0, n_rows=None) -> np.ndarray:
+    """Dequantise rows of ggml type t (12, 13, 14) to fp32."""
+    W, rows = _wt(W, K, t)
+    n_rows = rows - row0 if n_rows is None else n_rows
+    out = np.empty((n_rows, K), dtype=np.float32)
+    lib().orc_kq_dequant_rows_f32(_p(W), t, row0, n_rows, K, _p(out))
+    return out
+
+
+def kq_embed_rows_f16(W, K, t, ids) -> np.ndarray:
+    W, rows = _wt(W, K, t)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    out = np.empty((ids.size, K), dtype=np.uint16)
+    lib().orc_kq_embed_rows_f16(_p(W), t, rows, K, _p(ids), ids.size, _p(out))
+    return out
+
+
+def kq_gemv_f32(W, K, t, x16, row0=0, n_rows=None) -> np.ndarray:
+    """Reference CPU GEMV (gemv_quant_cpu) for ggml type t; x16 fp16 bits [K]."""
+    W, rows = _wt(W, K, t)
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    n_rows = rows - row0 if n_rows is None else n_rows
+    y = np.empty(n_rows, dtype=np.float32)
+    lib().orc_kq_gemv_f32(_p(W), t, _p(x16), row0, n_rows, K, _p(y))
+    return y
+
+
+def kq_gemm_f64(W, K, t, x32, wkind: str | None) -> np.ndarray:
+    """fp64 y[N, M] with weights rounded to 'f16' / 'bf16' / not at all (None)."""
+    W, rows = _wt(W, K, t)
+    x32 = np.ascontiguousarray(np.atleast_2d(x32), dtype=np.float32)
+    N = x32.shape[0]
+    y = np.empty((N, rows), dtype=np.float64)
+    kind = {"f16": 0, "bf16": 1, None: -1}[wkind]
+    lib().orc_kq_gemm_f64(_p(W), t, _p(x32), rows, N, K, kind, _p(y))
+    return y
 
 
 def f16_bits(a: np.ndarray) -> np.ndarray:

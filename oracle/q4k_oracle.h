@@ -26,6 +26,8 @@ extern "C" {
 
 #define ORC_QK_K 256
 #define ORC_BLOCK_BYTES 144
+#define ORC_Q5K_BYTES 176
+#define ORC_Q6K_BYTES 210
 
 /* fp16 bits -> fp32, host branch of raw_fp16_to_float (q4_gemm.cu:177-188). */
 float orc_fp16_to_f32(uint16_t h);
@@ -76,6 +78,18 @@ void orc_gemm_tokens_f32(const void *W, const uint16_t *x, int64_t M, int64_t N,
 /* fp64 reference for tolerance checks: y[row] = sum_k w32[row,k] * x[k],
  * accumulated in double, with w32 the exact fp32 dequantised weight and x
  * given as fp32 values (already rounded to whatever operand type is used). */
+/* Q5_K (ggml type 13) and Q6_K (14), kquant_oracle.c; type 12 forwards to
+ * the Q4_K functions above. */
+int orc_block_bytes(int ggml_type);
+void orc_kq_dequant_rows_f32(const void *W, int type, int64_t row0, int64_t n_rows, int K,
+                             float *out);
+void orc_kq_embed_rows_f16(const void *W, int type, int64_t n_rows, int K, const int32_t *ids,
+                           int64_t n_ids, uint16_t *out);
+void orc_kq_gemv_f32(const void *W, int type, const uint16_t *x, int64_t row0, int64_t n_rows,
+                     int K, float *y);
+void orc_kq_gemm_f64(const void *W, int type, const float *x, int64_t M, int64_t N, int K,
+                     int wkind, double *y);
+
 void orc_gemv_f64(const void *W, const float *x, int64_t M, int K, double *y);
 /* fp64 GEMM over operands rounded like the MFMA kernels: wr = round(w32) to
  * fp16 (wkind=0) or bf16 (wkind=1); x given as fp32 values [N x K];
