@@ -11,9 +11,11 @@
  * small-batch decode, the quantiser used to build inputs).
  *
  * Conventions for every entry point:
- *   - `w` is a DEVICE pointer to raw GGML Q4_K blocks (ggml_type 12): rows of
- *     K/256 blocks of 144 bytes, row-major, 16-byte aligned.  Pointer
- *     resolution of host/mmap pointers happens above this layer
+ *   - `w` is a DEVICE pointer to raw GGML blocks of `ggml_type`: Q4_K (12,
+ *     144 bytes per 256 weights), Q5_K (13, 176 bytes) or Q6_K (14, 210
+ *     bytes); rows of K/256 blocks, row-major, the base 16-byte aligned.
+ *     The embedding entry points take Q4_K and Q6_K, as the reference.
+ *     Pointer resolution of host/mmap pointers happens above this layer
  *     (rxq4_resolve_weights).
  *   - fp16/bf16 buffers are raw 16-bit patterns; x must be 16-byte aligned.
  *   - K must be a positive multiple of 256 and at most RXQ4_MAX_K.
@@ -45,6 +47,8 @@ extern "C" {
 #define RXQ4_STATUS_NOT_IMPLEMENTED 5
 
 #define RXQ4_GGML_TYPE_Q4_K 12
+#define RXQ4_GGML_TYPE_Q5_K 13
+#define RXQ4_GGML_TYPE_Q6_K 14
 #define RXQ4_MAX_K 65536
 
 /* Element types for the typed GEMM entry point. */
@@ -55,7 +59,7 @@ extern "C" {
 /* One output range of a multi-matrix GEMV sharing one x (pair = 2, triple = 3). */
 typedef struct rxq4_rows {
     void *y;           /* fp16 [M] */
-    const void *w;     /* device Q4_K blocks [M x K/256] */
+    const void *w;     /* device blocks of ggml_type [M x K/256] */
     int ggml_type;
     int M;
 } rxq4_rows;
@@ -70,7 +74,8 @@ int rxq4_gemv_f16(void *y, const void *w, int ggml_type, const void *x, int M, i
 int rxq4_gemv_add_f16(void *y, const void *w, int ggml_type, const void *x,
                       const void *residual, int M, int K, void *stream);
 
-/* 1..3 independent GEMVs sharing x, one launch.
+/* 1..3 independent GEMVs sharing x; the Q4_K ranges take one launch, each
+ * Q5_K / Q6_K range one more.
  * Replaces kernels::gemv_quant_pair (reference q4_gemm.cu:2047-2056) with
  * n_ranges = 2 and kernels::gemv_quant_triple (q4_gemm.cu:2058-2069) with 3. */
 int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, int K,

@@ -60,6 +60,18 @@ hipError_t launch_gemm(void *y, int y_dtype, const uint8_t *w, const void *x, in
 hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
                         int64_t n_vocab, int n_ids, int K, hipStream_t stream);
 
+// Q5_K (13) / Q6_K (14) GEMV of one range with the given epilogue.
+hipError_t launch_kq_gemv(int ggml_type, const GemvRange &r, const uint16_t *x, int K,
+                          int epilogue, hipStream_t stream);
+
+// Q5_K / Q6_K multi-token product for any N >= 1 (16-token chunks).
+hipError_t launch_kq_tokens(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,
+                            int x_dtype, int M, int N, int K, hipStream_t stream);
+
+// Q6_K embedding rows (as launch_embed).
+hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
+                           int64_t n_vocab, int n_ids, int K, hipStream_t stream);
+
 // fp32 rows -> Q4_K blocks.
 hipError_t launch_quantize(uint8_t *dst, const float *src, int64_t n_blocks,
                            hipStream_t stream);

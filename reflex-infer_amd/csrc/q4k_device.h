@@ -102,6 +102,15 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int 
     return __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, 0, 0);
 }
 
+// 4 and 8 bytes per lane from rsrc + voffset (dword-aligned voffset).
+__device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t rsrc, int voffset) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rsrc, voffset, 0, 0);
+}
+
+__device__ __forceinline__ u32x2 buffer_load8(__amdgpu_buffer_rsrc_t rsrc, int voffset) {
+    return __builtin_amdgcn_raw_buffer_load_b64(rsrc, voffset, 0, 0);
+}
+
 // 16 bytes per lane, global (rsrc + voffset) -> LDS at lds + 16 * lane.
 __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds,
                                                 int voffset) {

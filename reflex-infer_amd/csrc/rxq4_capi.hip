@@ -36,11 +36,14 @@ int from_hip(hipError_t e, const char *what) {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+bool kquant_type(int t) { return t == RXQ4_GGML_TYPE_Q5_K || t == RXQ4_GGML_TYPE_Q6_K; }
+
 // Checks shared by every weight-streaming entry point.
 int check_common(const char *fn, const void *w, int ggml_type, int K) {
-    if (ggml_type != RXQ4_GGML_TYPE_Q4_K)
+    if (ggml_type != RXQ4_GGML_TYPE_Q4_K && !kquant_type(ggml_type))
         return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT,
-                    "%s: ggml_type %d not supported (only Q4_K = 12)", fn, ggml_type);
+                    "%s: ggml_type %d not supported (Q4_K = 12, Q5_K = 13, Q6_K = 14)", fn,
+                    ggml_type);
     if (K <= 0 || K % 256 != 0 || K > RXQ4_MAX_K)
         return fail(RXQ4_STATUS_INVALID_ARGUMENT,
                     "%s: K=%d must be a positive multiple of 256 and <= %d", fn, K, RXQ4_MAX_K);
@@ -74,9 +77,14 @@ int gemv_single(const char *fn, void *y, const void *w, int ggml_type, const voi
     if (epi == rxq4::kEpiAdd && !residual)
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null residual", fn);
     if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
+    const rxq4::GemvRange range{static_cast<const uint8_t *>(w), y,
+                                static_cast<const uint16_t *>(residual), M};
+    if (kquant_type(ggml_type))
+        return from_hip(rxq4::launch_kq_gemv(ggml_type, range, static_cast<const uint16_t *>(x),
+                                             K, epi, static_cast<hipStream_t>(stream)),
+                        fn);
     rxq4::GemvParams p{};
-    p.r[0] = rxq4::GemvRange{static_cast<const uint8_t *>(w), y,
-                             static_cast<const uint16_t *>(residual), M};
+    p.r[0] = range;
     p.n_ranges = 1;
     p.total_rows = M;
     p.x = static_cast<const uint16_t *>(x);
@@ -111,7 +119,13 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
     const char *fn = "rxq4_gemv_multi_f16";
     if (!ranges || n_ranges < 1 || n_ranges > 3)
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ranges=%d must be 1..3", fn, n_ranges);
+    // Q4_K ranges share one launch; each Q5_K / Q6_K range is a launch of its
+    // own on the same stream (the reference's mixed Q4/Q4/Q6 triple is one
+    // launch, q4_gemm.cu:1157-1206; the outputs are independent either way).
     rxq4::GemvParams p{};
+    rxq4::GemvRange kq[3];
+    int kq_type[3];
+    int n_kq = 0;
     int64_t total = 0;
     for (int i = 0; i < n_ranges; ++i) {
         const rxq4_rows &r = ranges[i];
@@ -119,19 +133,36 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
         if (s != RXQ4_STATUS_SUCCESS) return s;
         if (r.M < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d M=%d < 0", fn, i, r.M);
         if (r.M > 0 && !r.y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d null y", fn, i);
-        p.r[i] = rxq4::GemvRange{static_cast<const uint8_t *>(r.w), r.y, nullptr, r.M};
-        total += r.M;
+        const rxq4::GemvRange g{static_cast<const uint8_t *>(r.w), r.y, nullptr, r.M};
+        if (kquant_type(r.ggml_type)) {
+            if (r.M > 0) {
+                kq[n_kq] = g;
+                kq_type[n_kq++] = r.ggml_type;
+            }
+        } else {
+            p.r[p.n_ranges++] = g;
+            total += r.M;
+        }
     }
     int s = check_x(fn, x);
     if (s != RXQ4_STATUS_SUCCESS) return s;
     if (total > 0x7FFFFFFF) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: too many rows", fn);
-    if (total == 0) return ok();
+    if (total == 0 && n_kq == 0) return ok();
     if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
-    p.n_ranges = n_ranges;
-    p.total_rows = (int)total;
-    p.x = static_cast<const uint16_t *>(x);
-    p.nb = K / 256;
-    return from_hip(rxq4::launch_gemv(p, rxq4::kEpiF16, static_cast<hipStream_t>(stream)), fn);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint16_t *xx = static_cast<const uint16_t *>(x);
+    if (total > 0) {
+        p.total_rows = (int)total;
+        p.x = xx;
+        p.nb = K / 256;
+        hipError_t e = rxq4::launch_gemv(p, rxq4::kEpiF16, st);
+        if (e != hipSuccess) return from_hip(e, fn);
+    }
+    for (int i = 0; i < n_kq; ++i) {
+        hipError_t e = rxq4::launch_kq_gemv(kq_type[i], kq[i], xx, K, rxq4::kEpiF16, st);
+        if (e != hipSuccess) return from_hip(e, fn);
+    }
+    return ok();
 }
 
 int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x, int x_dtype,
@@ -158,7 +189,10 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
                            y_dtype == RXQ4_DTYPE_F32 ? rxq4::kEpiF32 : rxq4::kEpiF16, stream);
     }
     hipError_t e;
-    if (N <= rxq4::kMaxSmallBatch)
+    if (kquant_type(ggml_type))
+        e = rxq4::launch_kq_tokens(ggml_type, y, y_dtype, static_cast<const uint8_t *>(w), x,
+                                   x_dtype, M, N, K, st);
+    else if (N <= rxq4::kMaxSmallBatch)
         e = rxq4::launch_gemv_tokens(y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M,
                                      N, K, st);
     else
@@ -180,15 +214,16 @@ int rxq4_embed_row_f16(void *dst, const void *w, int ggml_type, int token_id, in
     if (hidden_dim <= 0 || hidden_dim % 256 != 0)
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
     if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
-    if (ggml_type != RXQ4_GGML_TYPE_Q4_K)
+    // Q4_K and Q6_K, as the reference (q4_gemm.cu:2089-2106).
+    if (ggml_type != RXQ4_GGML_TYPE_Q4_K && ggml_type != RXQ4_GGML_TYPE_Q6_K)
         return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
     if (!aligned16(w) || !dst || !aligned16(dst))
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights/dst must be 16-byte aligned", fn);
     if (!rxq4::device_info().arch_ok)
         return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
-    return from_hip(rxq4::launch_embed(static_cast<uint16_t *>(dst),
-                                       static_cast<const uint8_t *>(w), nullptr, token_id, 0, 1,
-                                       hidden_dim, static_cast<hipStream_t>(stream)),
+    const auto launch = ggml_type == RXQ4_GGML_TYPE_Q6_K ? rxq4::launch_kq_embed : rxq4::launch_embed;
+    return from_hip(launch(static_cast<uint16_t *>(dst), static_cast<const uint8_t *>(w), nullptr,
+                           token_id, 0, 1, hidden_dim, static_cast<hipStream_t>(stream)),
                     fn);
 }
 
@@ -198,7 +233,7 @@ int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab
     if (hidden_dim <= 0 || hidden_dim % 256 != 0)
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
     if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
-    if (ggml_type != RXQ4_GGML_TYPE_Q4_K)
+    if (ggml_type != RXQ4_GGML_TYPE_Q4_K && ggml_type != RXQ4_GGML_TYPE_Q6_K)
         return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
     if (n_ids < 0 || n_vocab < 0)
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ids=%d n_vocab=%lld", fn, n_ids,
@@ -208,9 +243,9 @@ int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
     if (!rxq4::device_info().arch_ok)
         return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
-    return from_hip(rxq4::launch_embed(static_cast<uint16_t *>(dst),
-                                       static_cast<const uint8_t *>(w), ids, 0, n_vocab, n_ids,
-                                       hidden_dim, static_cast<hipStream_t>(stream)),
+    const auto launch = ggml_type == RXQ4_GGML_TYPE_Q6_K ? rxq4::launch_kq_embed : rxq4::launch_embed;
+    return from_hip(launch(static_cast<uint16_t *>(dst), static_cast<const uint8_t *>(w), ids, 0,
+                           n_vocab, n_ids, hidden_dim, static_cast<hipStream_t>(stream)),
                     fn);
 }
 

@@ -8,8 +8,8 @@
 //   * there is no CPU fallback: host-only weights (no GPU-visible alias) and
 //     launch errors return InvalidArgument with a one-time stderr message,
 //     where the reference would run gemv_quant_cpu;
-//   * only Q4_K (ggml_type 12) is implemented; other types return
-//     UnsupportedQuantFormat (the reference also serves Q5_K/Q6_K);
+//   * ggml types other than Q4_K/Q5_K/Q6_K (12/13/14) return
+//     UnsupportedQuantFormat, where the reference zero-fills y;
 //   * K must be a multiple of 256 (the reference assumes it silently);
 //   * JLLM_FAST_GEMV=0, which selects the reference's CPU path, is reported
 //     once and ignored; the CUDA variant switches (JLLM_Q4K_UINT32_LOADS,

@@ -79,9 +79,11 @@ def test_reference_dispatcher_runs_on_this_kernel_layer():
     ours = _nm(KLIB, "-D", "--defined-only")
     assert not any("reflex5infer10gemv_quantE" in s for s in ours)  # seam only, no API
     out = _probe(DISPATCH_ON_HIP)
-    # Q5_K through the reference dispatcher -> this seam: UnsupportedQuantFormat;
-    # attention -> this seam's NotImplemented; nothing registered.
-    assert out == {"gemv_quant_q5k": 3, "flash_attention_decode": 5, "registry_empty": 1}
+    # Through the reference dispatcher into this seam: Q8_K (15) ->
+    # UnsupportedQuantFormat, Q5_K with K=100 -> InvalidArgument (the type is
+    # served, the shape is not), attention -> NotImplemented; nothing registered.
+    assert out == {"gemv_quant_q8k": 3, "gemv_quant_q5k_bad_k": 4,
+                   "flash_attention_decode": 5, "registry_empty": 1}
 
 
 def test_library_exports_every_c_abi_entry_point():

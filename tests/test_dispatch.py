@@ -88,14 +88,17 @@ def test_empty_gemm_is_a_no_op():
 def test_c_abi_rejects_bad_arguments_before_launch():
     L = capi.lib()
     w = 0x10000  # never dereferenced: every call below fails validation first
-    assert L.rxq4_gemv_f16(w, w, 13, w, 4, 256, None) == rxq4.UNSUPPORTED_QUANT_FORMAT
+    assert L.rxq4_gemv_f16(w, w, 15, w, 4, 256, None) == rxq4.UNSUPPORTED_QUANT_FORMAT
+    assert L.rxq4_gemv_f16(w, w, 13, w, 4, 100, None) == rxq4.INVALID_ARGUMENT
+    assert L.rxq4_gemm_f16(w, w, 14, w, 4, 4, 100, None) == rxq4.INVALID_ARGUMENT
     assert L.rxq4_gemv_f16(w, w, 12, w, 4, 100, None) == rxq4.INVALID_ARGUMENT
     assert "K=100" in capi.last_error()
     assert L.rxq4_gemv_f32(w, w + 4, 12, w, 4, 256, None) == rxq4.INVALID_ARGUMENT
     assert L.rxq4_gemv_f16(w, w, 12, w, 4, 65536 + 256, None) == rxq4.INVALID_ARGUMENT
     assert L.rxq4_gemv_multi_f16(None, 0, w, 256, None) == rxq4.INVALID_ARGUMENT
     assert L.rxq4_embed_row_f16(w, w, 12, 0, 300, None) == rxq4.INVALID_ARGUMENT
-    assert L.rxq4_embed_row_f16(w, w, 14, 0, 256, None) == rxq4.UNSUPPORTED_QUANT_FORMAT
+    assert L.rxq4_embed_row_f16(w, w, 13, 0, 256, None) == rxq4.UNSUPPORTED_QUANT_FORMAT
+    assert L.rxq4_embed_rows_f16(w, w, 13, 8, w, 1, 256, None) == rxq4.UNSUPPORTED_QUANT_FORMAT
     assert L.rxq4_quantize_q4k(w, w, 4, 255, None) == rxq4.INVALID_ARGUMENT
     assert L.rxq4_gemm(w, 2, w, 12, w, 1, 4, 4, 256, None) == rxq4.INVALID_ARGUMENT  # bf16 y, f16 x
     assert L.rxq4_gemm(w, 1, w, 12, w + 8, 1, 4, 4, 256, None) == rxq4.INVALID_ARGUMENT

@@ -1,0 +1,162 @@
+"""GPU parity of the Q5_K (13) and Q6_K (14) kernels against the CPU oracle.
+
+Same bars as the Q4_K path (tests/util.py): embedding rows bit-exact;
+GEMV/GEMM within rel_err <= 1e-3 of the oracle over identically rounded
+operands, 16-bit outputs correctly rounded up to accumulation order.
+Weights are random blocks packed by index (tests/kquant_blocks.py): every
+quant value, scale and high-bit pattern occurs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import rxq4
+from oracle import oracle as orc
+from rxq4 import api, capi
+from tests import kquant_blocks as kb
+from tests import util
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host16(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint16)
+
+
+def f16(bits: np.ndarray) -> np.ndarray:
+    return bits.view(np.float16).astype(np.float32)
+
+
+# (rows, K): packed rows per wave step (K 2048 -> 2 rows, 256 -> 16 rows,
+# 4096 -> 1 row), long rows (11008: 172 slots, 1536: 24 slots), a partial last
+# step (37 rows), and a K whose x staging needs more than 64 KiB of LDS.
+GEMV_SHAPES = [(256, 2048), (300, 256), (37, 4096), (100, 11008), (64, 1536), (3, 32768)]
+
+
+@pytest.mark.parametrize("t", [13, 14])
+@pytest.mark.parametrize("M,K", GEMV_SHAPES)
+def test_kq_gemv_f32_f16(t, M, K):
+    print(f"kq gemv type {t} M={M} K={K}", flush=True)
+    Wn = kb.random_blocks(t, util.rng(700 + t + M), M, K)
+    x16 = util.x_f16(701 + K, K)
+    ref = orc.kq_gemv_f32(Wn, K, t, x16)
+    W, x = dev(Wn), dev(x16)
+    y32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    capi.gemv_f32(y32, W, x, M, K, ggml_type=t)
+    assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL
+    y16 = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_f16(y16, W, x, M, K, ggml_type=t)
+    assert util.rel_err(f16(host16(y16)), ref) <= util.TOL
+    assert util.rounded_ok(host16(y16), ref).all()
+
+
+@pytest.mark.parametrize("t", [13, 14])
+def test_kq_gemv_add_in_place(t):
+    M, K = 512, 2048
+    Wn = kb.random_blocks(t, util.rng(710 + t), M, K)
+    x16, res16 = util.x_f16(711, K), util.x_f16(712, M)
+    y32 = orc.kq_gemv_f32(Wn, K, t, x16)
+    W, x, res = dev(Wn), dev(x16), dev(res16)
+    a = api.GemvQuantAddArgs(y=res.data_ptr(), weights=W.data_ptr(), ggml_type=t,
+                             x=x.data_ptr(), residual=res.data_ptr(), M=M, K=K)
+    assert api.call("gemv_quant_add", a) == rxq4.SUCCESS
+    proj_sp = util.spacing(orc.f32_to_fp16(y32), "f16")
+    exact = y32.astype(np.float64) + f16(res16)
+    assert util.rounded_ok(host16(res), exact, extra=proj_sp / 2).all()
+
+
+def test_api_mixed_q4_q4_q6_triple():
+    """The Qwen3-4B fused QKV: Wq, Wk Q4_K, Wv Q6_K (reference
+    q4_gemm.cu:892-939)."""
+    K = 2048
+    Ms = (2048, 256, 256)
+    types = (12, 12, 14)
+    x16 = util.x_f16(720, K)
+    Wn = [util.weights(721, Ms[0], K), util.weights(722, Ms[1], K),
+          kb.random_blocks(14, util.rng(723), Ms[2], K)]
+    Wd = [dev(w) for w in Wn]
+    ys = [torch.empty(m, dtype=torch.float16, device="cuda") for m in Ms]
+    x = dev(x16)
+    a = api.GemvQuantTripleArgs(
+        y0=ys[0].data_ptr(), weights0=Wd[0].data_ptr(), ggml_type0=types[0], M0=Ms[0],
+        y1=ys[1].data_ptr(), weights1=Wd[1].data_ptr(), ggml_type1=types[1], M1=Ms[1],
+        y2=ys[2].data_ptr(), weights2=Wd[2].data_ptr(), ggml_type2=types[2], M2=Ms[2],
+        x=x.data_ptr(), K=K)
+    assert api.call("gemv_quant_triple", a) == rxq4.SUCCESS
+    for yv, w, t in zip(ys, Wn, types):
+        ref = orc.kq_gemv_f32(w, K, t, x16)
+        assert util.rounded_ok(host16(yv), ref).all()
+    # pair of two Q5_K matrices through the C ABI
+    W5 = [kb.random_blocks(13, util.rng(724 + i), 300, K) for i in range(2)]
+    y5 = [torch.empty(300, dtype=torch.float16, device="cuda") for _ in range(2)]
+    W5d = [dev(w) for w in W5]
+    capi.gemv_multi_f16([(y5[0], W5d[0], 300, 13), (y5[1], W5d[1], 300, 13)], x, K)
+    for yv, w in zip(y5, W5):
+        assert util.rounded_ok(host16(yv), orc.kq_gemv_f32(w, K, 13, x16)).all()
+
+
+@pytest.mark.parametrize("K", [256, 2048, 11008])
+def test_q6k_embedding_bit_exact(K):
+    V = 40
+    Wn = kb.random_blocks(14, util.rng(730 + K), V, K)
+    W = dev(Wn)
+    dst = torch.empty(K, dtype=torch.float16, device="cuda")
+    for tok in (0, 17, V - 1):
+        a = api.DequantEmbeddingRowArgs(dst=dst.data_ptr(), weights=W.data_ptr(), ggml_type=14,
+                                        token_id=tok, hidden_dim=K)
+        assert api.call("dequant_embedding_row", a) == rxq4.SUCCESS
+        want = orc.kq_embed_rows_f16(Wn, K, 14, np.array([tok], np.int32))[0]
+        assert np.array_equal(host16(dst), want)
+    ids = np.array([3, -1, V, 0, 39, 3, 12], np.int32)
+    out = torch.empty((ids.size, K), dtype=torch.float16, device="cuda")
+    capi.embed_rows_f16(out, W, V, dev(ids), K, ggml_type=14)
+    assert np.array_equal(host16(out), orc.kq_embed_rows_f16(Wn, K, 14, ids))
+
+
+@pytest.mark.parametrize("t", [13, 14])
+@pytest.mark.parametrize("M,N,K", [(300, 2, 2048), (129, 17, 512), (64, 40, 11008), (33, 5, 256)])
+def test_kq_gemm(t, M, N, K):
+    print(f"kq gemm type {t} M={M} N={N} K={K}", flush=True)
+    Wn = kb.random_blocks(t, util.rng(740 + t + N), M, K)
+    W = dev(Wn)
+    # bf16 activations, fp32 and bf16 outputs
+    xb = util.f32_to_bf16_bits(util.gaussian(741 + N, (N, K)))
+    xv = orc.bits_bf16_to_f32(xb)
+    ref = orc.kq_gemm_f64(Wn, K, t, xv, "bf16")
+    x = torch.from_numpy(xb.view(np.int16)).cuda().view(torch.bfloat16)
+    y32 = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    capi.gemm(y32, W, x, M, N, K, ggml_type=t)
+    assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL
+    yb = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+    capi.gemm(yb, W, x, M, N, K, ggml_type=t)
+    assert util.rounded_ok(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref, "bf16").all()
+    # the reference API: fp16 in and out
+    x16 = util.x_f16(742 + N, (N, K))
+    ref16 = orc.kq_gemm_f64(Wn, K, t, f16(x16), "f16")
+    y = torch.empty((N, M), dtype=torch.float16, device="cuda")
+    xd = dev(x16)
+    a = api.GemmQuantBatchedArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=t,
+                                 x=xd.data_ptr(), M=M, N=N, K=K)
+    assert api.call("gemm_quant_batched", a) == rxq4.SUCCESS
+    assert util.rounded_ok(host16(y), ref16).all()
+
+
+def test_kq_gemm_n1_is_the_gemv():
+    M, K = 200, 2048
+    Wn = kb.random_blocks(14, util.rng(750), M, K)
+    x16 = util.x_f16(751, (1, K))
+    W, x = dev(Wn), dev(x16)
+    y = torch.empty((1, M), dtype=torch.float16, device="cuda")
+    capi.gemm_f16(y, W, x, M, 1, K, ggml_type=14)
+    y2 = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_f16(y2, W, x, M, K, ggml_type=14)
+    assert torch.equal(y[0], y2)

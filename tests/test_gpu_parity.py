@@ -215,7 +215,7 @@ def test_api_gemv_pointer_resolution():
     a = api.GemvQuantArgs(y=y.data_ptr(), weights=host_ptr, ggml_type=12, x=x.data_ptr(),
                           M=M, K=K)
     assert api.call("gemv_quant", a) == rxq4.INVALID_ARGUMENT
-    a = api.GemvQuantArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=14, x=x.data_ptr(),
+    a = api.GemvQuantArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=15, x=x.data_ptr(),
                           M=M, K=K)
     assert api.call("gemv_quant", a) == rxq4.UNSUPPORTED_QUANT_FORMAT
     f = api.GemvQuantF32Args(y=torch.empty(M, device="cuda").data_ptr(), weights=W.data_ptr(),
