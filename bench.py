@@ -21,6 +21,8 @@ stream and timed with HIP events recorded on that stream around replays:
   per_kernel   every decode projection, the LM head [151936 x 2048] fp32
                GEMV, the 4096-id Zipf(1.1) embedding gather, and the prefill
                GEMM at m=512 (TFLOP/s, BASELINE metric's second half)
+  q6k_*        Q6_K (ggml type 14) LM head, embedding gather, down, and the
+               mixed Q4_K/Q4_K/Q6_K QKV triple (the Q4_K_M file layout)
   small_batch_decode  m in {1,2,4,8,16} tokens on gate+up and down
                (where weight reuse ends the purely
                bandwidth-bound regime)
@@ -335,6 +337,53 @@ def main() -> int:
         kernels["embed_gather_4096_zipf"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
                                              "unique_rows": uniq}
         del heads
+
+        # Q6_K (ggml type 14): LM head, embedding gather and ffn_down as a
+        # Q4_K_M file stores them, and the Qwen3-4B-style mixed QKV triple
+        # (Q4_K q, k + Q6_K v).  Random blocks with a fixed d (timing only).
+        def q6_blocks(seed, rows, K):
+            g = torch.Generator(device=dev).manual_seed(seed)
+            w = torch.randint(0, 256, (rows, K // 256, 210), generator=g, dtype=torch.uint8,
+                              device=dev)
+            w[:, :, 208], w[:, :, 209] = 0x00, 0x0C  # d = 2^-12
+            return w.reshape(rows, -1)
+
+        q6b = lambda rows, K: rows * (K // 256) * 210  # noqa: E731
+        heads6 = [q6_blocks(60_000 + i, VOCAB, HIDDEN) for i in range(2)]
+
+        def lm6_launch(i):
+            capi.gemv_f32(logits, heads6[i % 2], x_h, VOCAB, HIDDEN, stream=sp, ggml_type=14)
+        med, _ = per_launch(lm6_launch, 20)
+        b = q6b(VOCAB, HIDDEN) + 2 * HIDDEN + 4 * VOCAB
+        kernels["q6k_lm_head_f32_151936x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+
+        def emb6_launch(i):
+            capi.embed_rows_f16(emb, heads6[i % 2], VOCAB, ids, HIDDEN, stream=sp, ggml_type=14)
+        med, _ = per_launch(emb6_launch, 20)
+        b = uniq * q6b(1, HIDDEN) + 4096 * HIDDEN * 2 + 4096 * 4
+        kernels["q6k_embed_gather_4096_zipf"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+        del heads6
+
+        downs6 = [q6_blocks(61_000 + i, HIDDEN, FFN) for i in range(8)]
+
+        def d6_launch(i):
+            capi.gemv_add_f16(y_d, downs6[i % 8], x_f, res, HIDDEN, FFN, stream=sp, ggml_type=14)
+        med, _ = per_launch(d6_launch, 40)
+        b = q6b(HIDDEN, FFN) + 2 * FFN + 4 * HIDDEN
+        kernels["q6k_down_add_2048x11008"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+        del downs6
+
+        vs6 = [q6_blocks(62_000 + i, 256, HIDDEN) for i in range(8)]
+
+        def mixed_launch(i):
+            q = layers[i % N_LAYERS]["qkv"]
+            capi.gemv_multi_f16([(y_qkv[:2048], q[:2048], 2048), (y_qkv[2048:2304], q[2048:2304], 256),
+                                 (y_qkv[2304:], vs6[i % 8], 256, 14)], x_h, HIDDEN, stream=sp)
+        med, _ = per_launch(mixed_launch, 40)
+        b = qbytes(2304, HIDDEN) + q6b(256, HIDDEN) + 2 * HIDDEN + 2 * 2560
+        kernels["qkv_q4q4q6_2560x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
+                                           "launches": 2}
+        del vs6
 
         # Small-batch decode: m tokens through
         # gemm_quant_batched's C-ABI form with fp16 x / y on the decode
