@@ -57,6 +57,9 @@ def lib() -> ctypes.CDLL:
             "orc_kq_embed_rows_f16": (None, [P, I, I64, I, P, I64, P]),
             "orc_kq_gemv_f32": (None, [P, I, P, I64, I64, I, P]),
             "orc_kq_gemm_f64": (None, [P, I, P, I64, I64, I, I, P]),
+            "orc_attn_decode_f32": (None, [P, P, P, I, I, I, I, ctypes.c_float, I, P, P, P]),
+            "orc_attn_prefill_f32": (None, [P, P, P, I, I, I, I, I, ctypes.c_float, I, P, P, P]),
+            "orc_attn_decode_f64": (None, [P, P, P, I, I, I, I, ctypes.c_double, I, P, P, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -261,6 +264,52 @@ def kq_gemm_f64(W, K, t, x32, wkind: str | None) -> np.ndarray:
     kind = {"f16": 0, "bf16": 1, None: -1}[wkind]
     lib().orc_kq_gemm_f64(_p(W), t, _p(x32), rows, N, K, kind, _p(y))
     return y
+
+
+# ---------------------------------------------------------------- attention
+def _kv(k, kv_int8):
+    return np.ascontiguousarray(k, dtype=np.int8 if kv_int8 else np.uint16)
+
+
+def attn_decode_f32(q16, k, v, n_heads, n_kv, head_dim, seq_len, scale, kv_int8=False,
+                    ks=None, vs=None) -> np.ndarray:
+    """Reference CPU decode attention; q16 fp16 bits [n_heads*head_dim]; k, v
+    fp16 bits (uint16) or int8 [seq_len, n_kv, head_dim]."""
+    q16 = np.ascontiguousarray(q16, dtype=np.uint16)
+    k, v = _kv(k, kv_int8), _kv(v, kv_int8)
+    ks = None if ks is None else np.ascontiguousarray(ks, dtype=np.float32)
+    vs = None if vs is None else np.ascontiguousarray(vs, dtype=np.float32)
+    out = np.empty(n_heads * head_dim, dtype=np.float32)
+    lib().orc_attn_decode_f32(_p(q16), _p(k), _p(v), n_heads, n_kv, head_dim, seq_len, scale,
+                              int(kv_int8), None if ks is None else _p(ks),
+                              None if vs is None else _p(vs), _p(out))
+    return out
+
+
+def attn_prefill_f32(q16, k, v, n_heads, n_kv, head_dim, n_tok, start_pos, scale,
+                     kv_int8=False, ks=None, vs=None) -> np.ndarray:
+    q16 = np.ascontiguousarray(q16, dtype=np.uint16)
+    k, v = _kv(k, kv_int8), _kv(v, kv_int8)
+    ks = None if ks is None else np.ascontiguousarray(ks, dtype=np.float32)
+    vs = None if vs is None else np.ascontiguousarray(vs, dtype=np.float32)
+    out = np.empty(n_tok * n_heads * head_dim, dtype=np.float32)
+    lib().orc_attn_prefill_f32(_p(q16), _p(k), _p(v), n_heads, n_kv, head_dim, n_tok, start_pos,
+                               scale, int(kv_int8), None if ks is None else _p(ks),
+                               None if vs is None else _p(vs), _p(out))
+    return out
+
+
+def attn_decode_f64(q16, k, v, n_heads, n_kv, head_dim, seq_len, scale, kv_int8=False,
+                    ks=None, vs=None) -> np.ndarray:
+    q16 = np.ascontiguousarray(q16, dtype=np.uint16)
+    k, v = _kv(k, kv_int8), _kv(v, kv_int8)
+    ks = None if ks is None else np.ascontiguousarray(ks, dtype=np.float32)
+    vs = None if vs is None else np.ascontiguousarray(vs, dtype=np.float32)
+    out = np.empty(n_heads * head_dim, dtype=np.float64)
+    lib().orc_attn_decode_f64(_p(q16), _p(k), _p(v), n_heads, n_kv, head_dim, seq_len, scale,
+                              int(kv_int8), None if ks is None else _p(ks),
+                              None if vs is None else _p(vs), _p(out))
+    return out
 
 
 def f16_bits(a: np.ndarray) -> np.ndarray:

@@ -90,6 +90,19 @@ void orc_kq_gemv_f32(const void *W, int type, const uint16_t *x, int64_t row0, i
 void orc_kq_gemm_f64(const void *W, int type, const float *x, int64_t M, int64_t N, int K,
                      int wkind, double *y);
 
+/* Decode / prefill attention, attn_oracle.c.  q fp16 bits [n_heads x
+ * head_dim] (prefill: [n_tok x ...]); k, v fp16 bits or int8 [pos x n_kv x
+ * head_dim]; out fp32. */
+void orc_attn_decode_f32(const uint16_t *q, const void *k, const void *v, int n_heads, int n_kv,
+                         int head_dim, int seq_len, float scale, int kv_int8, const float *ks,
+                         const float *vs, float *out);
+void orc_attn_prefill_f32(const uint16_t *q, const void *k, const void *v, int n_heads, int n_kv,
+                          int head_dim, int n_tok, int start_pos, float scale, int kv_int8,
+                          const float *ks, const float *vs, float *out);
+void orc_attn_decode_f64(const uint16_t *q, const void *k, const void *v, int n_heads, int n_kv,
+                         int head_dim, int seq_len, double scale, int kv_int8, const float *ks,
+                         const float *vs, double *out);
+
 void orc_gemv_f64(const void *W, const float *x, int64_t M, int K, double *y);
 /* fp64 GEMM over operands rounded like the MFMA kernels: wr = round(w32) to
  * fp16 (wkind=0) or bf16 (wkind=1); x given as fp32 values [N x K];
