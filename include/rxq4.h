@@ -113,6 +113,30 @@ int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab
 /* NEW.  Quantise fp32 rows [n_rows x K] (device) to Q4_K blocks (device). */
 int rxq4_quantize_q4k(void *dst, const float *src, int64_t n_rows, int K, void *stream);
 
+/* out[n_heads x head_dim] fp16 = attention of one query token over KV
+ * positions [0, seq_len): per head h (KV head h / (n_heads / n_kv_heads)),
+ * softmax(scale * q.K^T) V with fp32 softmax.  k_cache / v_cache are
+ * [pos][n_kv_heads][head_dim], fp16, or int8 when kv_int8 != 0 with optional
+ * per-(position, KV head) fp32 scales k_scales / v_scales [pos][n_kv_heads]
+ * (NULL = 1).  head_dim a multiple of 8 (int8: 16), at most 256; n_heads a
+ * multiple of n_kv_heads.  Decode splits long sequences over the per-device
+ * workspace described above.
+ * Replaces kernels::flash_attention_decode (reference attention.cu:450-466,
+ * 41-173). */
+int rxq4_attention_decode_f16(void *out, const void *q, const void *k_cache,
+                              const void *v_cache, int n_heads, int n_kv_heads, int head_dim,
+                              int seq_len, float scale, int kv_int8, const float *k_scales,
+                              const float *v_scales, void *stream);
+
+/* Prefill: N query tokens q[N x n_heads x head_dim]; token t attends to
+ * positions [0, start_pos + t + 1) of the caches (causal).
+ * Replaces kernels::flash_attention_prefill_batched (reference
+ * attention.cu:432-448, 180-290). */
+int rxq4_attention_prefill_f16(void *out, const void *q, const void *k_cache,
+                               const void *v_cache, int n_heads, int n_kv_heads, int head_dim,
+                               int N, int start_pos, float scale, int kv_int8,
+                               const float *k_scales, const float *v_scales, void *stream);
+
 /* Pointer resolution of the reference (q4_gemm.cu:111-135): returns
  * w_device if non-NULL, else w if the HIP runtime reports it as device or
  * managed memory, else NULL (host-only memory cannot be read by the kernels). */

@@ -573,7 +573,7 @@ struct SplitWorkspace {
 static std::mutex g_ws_mutex;
 static SplitWorkspace g_ws[64];
 
-static hipError_t split_workspace(size_t bytes, float **ws) {
+hipError_t device_workspace(size_t bytes, float **ws) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -632,7 +632,7 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     p.splits = splits;
     if (splits > 1) {
         const size_t part = (size_t)tiles * splits * TM * kRowsPerWg * sizeof(float);
-        hipError_t e = split_workspace(part, &p.ws);
+        hipError_t e = device_workspace(part, &p.ws);
         if (e != hipSuccess) return e;
     }
     p.total_units = tiles * splits;

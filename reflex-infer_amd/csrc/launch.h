@@ -72,6 +72,17 @@ hipError_t launch_kq_tokens(int ggml_type, void *y, int y_dtype, const uint8_t *
 hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
                            int64_t n_vocab, int n_ids, int K, hipStream_t stream);
 
+// The per-device fp32 workspace (split-K partials, attention chunks):
+// allocated on first use, grown with a device synchronise, held until exit.
+hipError_t device_workspace(size_t bytes, float **ws);
+
+// Attention for n_tok query tokens; token t sees positions [0, seq0 + t).
+// Decode is n_tok = 1, seq0 = seq_len; prefill seq0 = start_pos + 1.
+hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, const void *v,
+                            const float *ks, const float *vs, int n_heads, int n_kv,
+                            int head_dim, int n_tok, int seq0, float scale, int kv_int8,
+                            hipStream_t stream);
+
 // fp32 rows -> Q4_K blocks.
 hipError_t launch_quantize(uint8_t *dst, const float *src, int64_t n_blocks,
                            hipStream_t stream);

@@ -264,6 +264,64 @@ int rxq4_quantize_q4k(void *dst, const float *src, int64_t n_rows, int K, void *
                     fn);
 }
 
+}  // extern "C"
+
+namespace {
+
+int attention(const char *fn, void *out, const void *q, const void *k, const void *v,
+              int n_heads, int n_kv, int head_dim, int n_tok, int seq0, float scale, int kv_int8,
+              const float *ks, const float *vs, void *stream) {
+    if (n_heads == 0 || n_tok == 0) return ok();
+    if (n_heads < 0 || n_kv <= 0 || n_heads % n_kv != 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT,
+                    "%s: n_heads=%d must be a positive multiple of n_kv_heads=%d", fn, n_heads,
+                    n_kv);
+    const int align = kv_int8 ? 16 : 8;
+    if (head_dim <= 0 || head_dim > 256 || head_dim % align != 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT,
+                    "%s: head_dim=%d must be a multiple of %d and <= 256", fn, head_dim, align);
+    if (n_tok < 0 || seq0 < 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: negative length", fn);
+    if (!out || !q || !aligned16(out) || !aligned16(q))
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: q/out null or not 16-byte aligned", fn);
+    if (seq0 + n_tok - 1 > 0 && (!k || !v || !aligned16(k) || !aligned16(v)))
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: k/v null or not 16-byte aligned", fn);
+    int s = check_device(fn);
+    if (s != RXQ4_STATUS_SUCCESS) return s;
+    return from_hip(rxq4::launch_attention(static_cast<uint16_t *>(out),
+                                           static_cast<const uint16_t *>(q), k, v,
+                                           kv_int8 ? ks : nullptr, kv_int8 ? vs : nullptr, n_heads,
+                                           n_kv, head_dim, n_tok, seq0, scale, kv_int8 ? 1 : 0,
+                                           static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rxq4_attention_decode_f16(void *out, const void *q, const void *k_cache,
+                              const void *v_cache, int n_heads, int n_kv_heads, int head_dim,
+                              int seq_len, float scale, int kv_int8, const float *k_scales,
+                              const float *v_scales, void *stream) {
+    if (seq_len < 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "rxq4_attention_decode_f16: seq_len=%d",
+                    seq_len);
+    return attention("rxq4_attention_decode_f16", out, q, k_cache, v_cache, n_heads, n_kv_heads,
+                     head_dim, 1, seq_len, scale, kv_int8, k_scales, v_scales, stream);
+}
+
+int rxq4_attention_prefill_f16(void *out, const void *q, const void *k_cache,
+                               const void *v_cache, int n_heads, int n_kv_heads, int head_dim,
+                               int N, int start_pos, float scale, int kv_int8,
+                               const float *k_scales, const float *v_scales, void *stream) {
+    if (N < 0 || start_pos < 0)
+        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "rxq4_attention_prefill_f16: N=%d start_pos=%d",
+                    N, start_pos);
+    return attention("rxq4_attention_prefill_f16", out, q, k_cache, v_cache, n_heads, n_kv_heads,
+                     head_dim, N, start_pos + 1, scale, kv_int8, k_scales, v_scales, stream);
+}
+
 const void *rxq4_resolve_weights(const void *w, const void *w_device) {
     if (w_device) return w_device;
     if (!w) return nullptr;

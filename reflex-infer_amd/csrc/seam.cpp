@@ -132,12 +132,20 @@ Status dequant_embedding_row(const DequantEmbeddingRowArgs& a) {
                   "dequant_embedding_row");
 }
 
-// Attention is outside the Q4 weight path; like the reference's no-CUDA
-// build (src/kernels/cuda_stubs.cpp:31-37) it reports NotImplemented.
-Status flash_attention_decode(const AttentionDecodeArgs&) { return Status::NotImplemented; }
+// Attention (reference attention.cu:432-466): the caches and q are device
+// pointers; no pointer resolution.
+Status flash_attention_decode(const AttentionDecodeArgs& a) {
+    return finish(rxq4_attention_decode_f16(a.output, a.q, a.k_cache, a.v_cache, a.n_heads,
+                                            a.n_kv_heads, a.head_dim, a.seq_len, a.scale,
+                                            a.kv_int8 ? 1 : 0, a.k_scales, a.v_scales, a.stream),
+                  "flash_attention_decode");
+}
 
-Status flash_attention_prefill_batched(const AttentionPrefillBatchedArgs&) {
-    return Status::NotImplemented;
+Status flash_attention_prefill_batched(const AttentionPrefillBatchedArgs& a) {
+    return finish(rxq4_attention_prefill_f16(a.output, a.q, a.k_cache, a.v_cache, a.n_heads,
+                                             a.n_kv_heads, a.head_dim, a.N, a.start_pos, a.scale,
+                                             a.kv_int8 ? 1 : 0, a.k_scales, a.v_scales, a.stream),
+                  "flash_attention_prefill_batched");
 }
 
 }  // namespace reflex::infer::kernels

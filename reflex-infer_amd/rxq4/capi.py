@@ -35,6 +35,12 @@ SIGNATURES = {
     "rxq4_embed_rows_f16": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int, c_int,
                                     c_void_p]),
     "rxq4_quantize_q4k": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p]),
+    "rxq4_attention_decode_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                          c_int, c_int, ctypes.c_float, c_int, c_void_p,
+                                          c_void_p, c_void_p]),
+    "rxq4_attention_prefill_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                           c_int, c_int, c_int, ctypes.c_float, c_int, c_void_p,
+                                           c_void_p, c_void_p]),
     "rxq4_resolve_weights": (c_void_p, [c_void_p, c_void_p]),
     "rxq4_version": (ctypes.c_char_p, []),
     "rxq4_last_error": (ctypes.c_char_p, []),
@@ -143,3 +149,18 @@ def quantize(src: torch.Tensor, stream=None) -> torch.Tensor:
     dst = torch.empty((rows, (K // 256) * 144), dtype=torch.uint8, device=src.device)
     quantize_q4k(dst, src.contiguous(), rows, K, stream)
     return dst
+
+
+def attention_decode_f16(out, q, k, v, n_heads, n_kv_heads, head_dim, seq_len, scale,
+                         kv_int8=False, k_scales=None, v_scales=None, stream=None):
+    return _check(lib().rxq4_attention_decode_f16(
+        _ptr(out), _ptr(q), _ptr(k), _ptr(v), n_heads, n_kv_heads, head_dim, seq_len, scale,
+        int(kv_int8), _ptr(k_scales), _ptr(v_scales), _stream(stream)), "rxq4_attention_decode_f16")
+
+
+def attention_prefill_f16(out, q, k, v, n_heads, n_kv_heads, head_dim, N, start_pos, scale,
+                          kv_int8=False, k_scales=None, v_scales=None, stream=None):
+    return _check(lib().rxq4_attention_prefill_f16(
+        _ptr(out), _ptr(q), _ptr(k), _ptr(v), n_heads, n_kv_heads, head_dim, N, start_pos, scale,
+        int(kv_int8), _ptr(k_scales), _ptr(v_scales), _stream(stream)),
+        "rxq4_attention_prefill_f16")

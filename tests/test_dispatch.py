@@ -74,10 +74,19 @@ def test_null_member_restores_builtin_slot():
                     api.DequantEmbeddingRowArgs(hidden_dim=0)) == rxq4.INVALID_ARGUMENT
 
 
-def test_attention_is_not_pluggable_and_not_implemented():
-    assert api.call("flash_attention_decode", api.AttentionDecodeArgs()) == rxq4.NOT_IMPLEMENTED
+def test_attention_validates_before_launch():
+    # no heads: nothing to do (the reference returns Success for every call)
+    assert api.call("flash_attention_decode", api.AttentionDecodeArgs()) == rxq4.SUCCESS
     assert api.call("flash_attention_prefill_batched",
-                    api.AttentionPrefillBatchedArgs()) == rxq4.NOT_IMPLEMENTED
+                    api.AttentionPrefillBatchedArgs()) == rxq4.SUCCESS
+    # shape errors are reported before any HIP call
+    bad_gqa = api.AttentionDecodeArgs(n_heads=6, n_kv_heads=4, head_dim=64, seq_len=8)
+    assert api.call("flash_attention_decode", bad_gqa) == rxq4.INVALID_ARGUMENT
+    bad_dim = api.AttentionPrefillBatchedArgs(n_heads=8, n_kv_heads=2, head_dim=72, N=2,
+                                             kv_int8=True)
+    assert api.call("flash_attention_prefill_batched", bad_dim) == rxq4.INVALID_ARGUMENT
+    too_big = api.AttentionDecodeArgs(n_heads=8, n_kv_heads=8, head_dim=512, seq_len=8)
+    assert api.call("flash_attention_decode", too_big) == rxq4.INVALID_ARGUMENT
 
 
 def test_empty_gemm_is_a_no_op():
