@@ -9,10 +9,12 @@
 //
 // A workgroup (4 waves) takes one KV head, up to 8 of its query heads, one
 // token and one chunk of positions, so each K/V row is read once for the
-// whole GQA group.  Positions are walked in tiles of 256 with an online
-// softmax:
-//   scores  a thread per position: its K row (16-byte loads) against the
-//           group's q (fp32 in LDS, read as broadcasts);
+// whole GQA group.  Positions are walked in tiles of 64 with an online
+// softmax (short tiles keep the serial latency of a workgroup low; decode
+// spreads a sequence over about four workgroups per CU):
+//   scores  16 lanes per position, 8 dims a lane (q of the group's heads
+//           in registers), the lanes' partial dots summed with DPP row
+//           rotations; the 16 positions of a lane group are loaded first;
 //   softmax 32 threads per head: tile max, rescale factor, exp and sum;
 //   P.V     a thread per fp16 pair of dims and per quarter of the tile (V rows
 //           read 256 bytes per wave per position), partials added across the
@@ -29,7 +31,7 @@
 
 namespace rxq4 {
 
-constexpr int kAttnTile = 256;
+constexpr int kAttnTile = 64;
 constexpr int kAttnMaxHeads = 8;   // query heads per workgroup
 constexpr int kAttnMaxDim = 256;
 
@@ -46,8 +48,46 @@ struct AttnParams {
     int kv_int8;
 };
 
+// Sum over the 16 lanes of a DPP row (every lane gets the sum).
+template <int CTRL>
+__device__ __forceinline__ float row_ror_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v = row_ror_add<0x128>(v);  // row_ror:8
+    v = row_ror_add<0x124>(v);  // row_ror:4
+    v = row_ror_add<0x122>(v);  // row_ror:2
+    return row_ror_add<0x121>(v);  // row_ror:1
+}
+
+// 8 dims of a K/V row as fp32: fp16 (16 bytes) or int8 (8 bytes).
+__device__ __forceinline__ void kv8(const void *row, int kv_int8, int chunk, float *f) {
+    if (!kv_int8) {
+        const u32x4 w = reinterpret_cast<const u32x4 *>(row)[chunk];
+        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            f[2 * e] = f16_bits_to_f32(wv[e] & 0xFFFFu);
+            f[2 * e + 1] = f16_bits_to_f32(wv[e] >> 16);
+        }
+    } else {
+        const u32x2 w = reinterpret_cast<const u32x2 *>(row)[chunk];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            f[e] = (float)(int8_t)(uint8_t)((e < 4 ? w.x : w.y) >> (8 * (e & 3)));
+    }
+}
+
+// CPL = 8-dim chunks per lane (1: head_dim <= 128, 2: <= 256); HPW = query
+// heads per workgroup, a power of two (q is zero for heads past the group,
+// whose results are not stored), so every head loop is unrolled without
+// branches; the positions per load batch (PB) shrink with CPL so q and the
+// raw K rows stay in registers.
+template <int CPL, int HPW>
 __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
-    __shared__ float qf[kAttnMaxHeads][kAttnMaxDim];
+    constexpr int MAXH = HPW;
+    constexpr int PPG = kAttnTile / 16;  // positions per lane group
     __shared__ float sc[kAttnMaxHeads][kAttnTile];
     __shared__ float stat[3][kAttnMaxHeads];  // running max, running sum, rescale
     __shared__ float red[4][kAttnMaxHeads][kAttnMaxDim];
@@ -66,84 +106,94 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
     const int end = min(seq, beg + p.chunk);
     const int hd = p.head_dim;
     const int64_t q_dim = (int64_t)p.n_heads * hd;
+    const int esz = p.kv_int8 ? 1 : 2;  // bytes per K/V element
 
-    for (int i = tid; i < nh * hd; i += 256)
-        qf[i / hd][i % hd] = f16_bits_to_f32(p.q[t * q_dim + (int64_t)h0 * hd + i]);
+    // Scores layout: lane group grp (16 lanes) takes positions grp + 16 i;
+    // lane sub holds dims 8 (sub + 16 j), j < cpl.
+    const int sub = tid & 15, grp = tid >> 4;
+    const int n8 = hd >> 3;  // 8-dim chunks per row
+    float qr[CPL][MAXH][8];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int h = 0; h < MAXH; ++h) {
+            const int ch = sub + 16 * j;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                qr[j][h][e] = (h < nh && ch < n8)
+                                  ? f16_bits_to_f32(p.q[t * q_dim + (int64_t)(h0 + h) * hd + 8 * ch + e])
+                                  : 0.0f;
+        }
     if (tid < kAttnMaxHeads) {
         stat[0][tid] = -INFINITY;
         stat[1][tid] = 0.0f;
     }
     // P.V: this thread's fp16 dim pairs (pp, pp + 64) for the quarter wq.
     const int npairs = hd >> 1;
-    float acc[kAttnMaxHeads][2][2];
+    float acc[MAXH][CPL][2];
 #pragma unroll
-    for (int h = 0; h < kAttnMaxHeads; ++h)
+    for (int h = 0; h < MAXH; ++h)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[h][j][0] = acc[h][j][1] = 0.0f;
+        for (int j = 0; j < CPL; ++j) acc[h][j][0] = acc[h][j][1] = 0.0f;
     __syncthreads();
 
     const int64_t row_stride = (int64_t)p.n_kv * hd;  // elements per position
+    const uint8_t *kb = static_cast<const uint8_t *>(p.k) + (int64_t)kvh * hd * esz;
+    const uint8_t *vb = static_cast<const uint8_t *>(p.v) + (int64_t)kvh * hd * esz;
     for (int p0 = beg; p0 < end; p0 += kAttnTile) {
-        // Scores: thread tid = position p0 + tid.
+        // Scores: PPG positions per lane group, loads first.  Positions past
+        // the end re-read the last valid row and score -inf.
         {
-            const int pos = p0 + tid;
-            float dot[kAttnMaxHeads];
+            constexpr int i0 = 0, PB = PPG;
+            u32x4 raw[PB][CPL];
 #pragma unroll
-            for (int h = 0; h < kAttnMaxHeads; ++h) dot[h] = 0.0f;
-            if (pos < end) {
-                const int64_t base = pos * row_stride + (int64_t)kvh * hd;
-                if (!p.kv_int8) {
-                    const u32x4 *kr = reinterpret_cast<const u32x4 *>(
-                        static_cast<const uint16_t *>(p.k) + base);
-                    for (int d8 = 0; d8 < hd / 8; ++d8) {
-                        const u32x4 w = kr[d8];
-                        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-                        float kf[8];
+            for (int i = 0; i < PB; ++i) {
+                const int pos = min(p0 + grp + 16 * (i0 + i), end - 1);
+                const uint8_t *row = kb + pos * row_stride * esz;
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            kf[2 * i] = f16_bits_to_f32(wv[i] & 0xFFFFu);
-                            kf[2 * i + 1] = f16_bits_to_f32(wv[i] >> 16);
-                        }
-#pragma unroll
-                        for (int h = 0; h < kAttnMaxHeads; ++h) {
-                            if (h < nh) {
-#pragma unroll
-                                for (int i = 0; i < 8; ++i) dot[h] += qf[h][8 * d8 + i] * kf[i];
-                            }
-                        }
+                for (int j = 0; j < CPL; ++j) {
+                    const int ch = min(sub + 16 * j, n8 - 1);
+                    if (!p.kv_int8) {
+                        raw[i][j] = reinterpret_cast<const u32x4 *>(row)[ch];
+                    } else {
+                        const u32x2 w = reinterpret_cast<const u32x2 *>(row)[ch];
+                        raw[i][j] = u32x4{w.x, w.y, 0u, 0u};
                     }
-                } else {
-                    const u32x4 *kr = reinterpret_cast<const u32x4 *>(
-                        static_cast<const int8_t *>(p.k) + base);
-                    for (int d16 = 0; d16 < hd / 16; ++d16) {
-                        const u32x4 w = kr[d16];
-                        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-                        float kf[16];
-#pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                            kf[i] = (float)(int8_t)(uint8_t)(wv[i >> 2] >> (8 * (i & 3)));
-#pragma unroll
-                        for (int h = 0; h < kAttnMaxHeads; ++h) {
-                            if (h < nh) {
-#pragma unroll
-                                for (int i = 0; i < 16; ++i) dot[h] += qf[h][16 * d16 + i] * kf[i];
-                            }
-                        }
-                    }
-                    const float s = p.ks ? p.ks[(int64_t)pos * p.n_kv + kvh] : 1.0f;
-#pragma unroll
-                    for (int h = 0; h < kAttnMaxHeads; ++h) dot[h] *= s;
                 }
             }
 #pragma unroll
-            for (int h = 0; h < kAttnMaxHeads; ++h)
-                if (h < nh) sc[h][tid] = pos < end ? dot[h] * p.scale : -INFINITY;
+            for (int i = 0; i < PB; ++i) {
+                const int pos = p0 + grp + 16 * (i0 + i);
+                const float ks = (p.kv_int8 && p.ks && pos < end)
+                                     ? p.ks[(int64_t)pos * p.n_kv + kvh] : 1.0f;
+                float kf[CPL][8];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const uint32_t wv[4] = {raw[i][j].x, raw[i][j].y, raw[i][j].z, raw[i][j].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        kf[j][e] = p.kv_int8
+                                       ? (float)(int8_t)(uint8_t)(wv[e >> 2] >> (8 * (e & 3)))
+                                       : f16_bits_to_f32((wv[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+                }
+#pragma unroll
+                for (int h = 0; h < MAXH; ++h) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) d += qr[j][h][e] * kf[j][e];
+                    d = row16_sum(d);
+                    if (sub == 0)
+                        sc[h][grp + 16 * (i0 + i)] = pos < end ? d * ks * p.scale : -INFINITY;
+                }
+            }
         }
         __syncthreads();
         // Online softmax: 32 threads per head.
         {
             const int h = tid >> 5, l32 = tid & 31;
-            if (h < nh) {
+            if (h < HPW) {
                 float mx = -INFINITY;
                 for (int j = l32; j < kAttnTile; j += 32) mx = fmaxf(mx, sc[h][j]);
 #pragma unroll
@@ -173,51 +223,57 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
             }
         }
         __syncthreads();
-        // P.V over this thread's quarter of the tile.
+        // P.V over this thread's quarter of the tile: its 16 positions' V
+        // loads issued first (positions past q1 re-read the last valid row
+        // and are skipped), probabilities read 4 at a time.
         {
-            const int q0 = p0 + wq * 64;
-            const int q1 = min(end, q0 + 64);
+            const int q0 = p0 + wq * (kAttnTile / 4);
+            const int q1 = min(end, q0 + kAttnTile / 4);
 #pragma unroll
-            for (int h = 0; h < kAttnMaxHeads; ++h) {
-                if (h < nh) {
-                    const float corr = stat[2][h];
+            for (int h = 0; h < MAXH; ++h) {
+                const float corr = stat[2][h];
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        acc[h][j][0] *= corr;
-                        acc[h][j][1] *= corr;
-                    }
+                for (int j = 0; j < CPL; ++j) {
+                    acc[h][j][0] *= corr;
+                    acc[h][j][1] *= corr;
                 }
             }
-            for (int pos = q0; pos < q1; ++pos) {
-                const int64_t base = pos * row_stride + (int64_t)kvh * hd;
-                float vf[2][2];
+            for (int pb = q0; pb < q1; pb += 16) {
+                float vf[16][CPL][2];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int pp = lane + 64 * j;
-                    vf[j][0] = vf[j][1] = 0.0f;
-                    if (pp < npairs) {
+                for (int i = 0; i < 16; ++i) {
+                    const int pos = min(pb + i, q1 - 1);
+                    const uint8_t *row = vb + pos * row_stride * esz;
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) {
+                        const int pp = min(lane + 64 * j, npairs - 1);
                         if (!p.kv_int8) {
-                            const uint32_t w =
-                                reinterpret_cast<const uint32_t *>(
-                                    static_cast<const uint16_t *>(p.v) + base)[pp];
-                            vf[j][0] = f16_bits_to_f32(w & 0xFFFFu);
-                            vf[j][1] = f16_bits_to_f32(w >> 16);
+                            const uint32_t w = reinterpret_cast<const uint32_t *>(row)[pp];
+                            vf[i][j][0] = f16_bits_to_f32(w & 0xFFFFu);
+                            vf[i][j][1] = f16_bits_to_f32(w >> 16);
                         } else {
-                            const uint16_t w = reinterpret_cast<const uint16_t *>(
-                                static_cast<const int8_t *>(p.v) + base)[pp];
-                            vf[j][0] = (float)(int8_t)(uint8_t)(w & 0xFFu);
-                            vf[j][1] = (float)(int8_t)(uint8_t)(w >> 8);
+                            const uint16_t w = reinterpret_cast<const uint16_t *>(row)[pp];
+                            vf[i][j][0] = (float)(int8_t)(uint8_t)(w & 0xFFu);
+                            vf[i][j][1] = (float)(int8_t)(uint8_t)(w >> 8);
                         }
                     }
                 }
 #pragma unroll
-                for (int h = 0; h < kAttnMaxHeads; ++h) {
-                    if (h < nh) {
-                        const float pr = sc[h][pos - p0];
+                for (int h = 0; h < MAXH; ++h) {
+                    const float4 *pr4 = reinterpret_cast<const float4 *>(&sc[h][pb - p0]);
 #pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            acc[h][j][0] += pr * vf[j][0];
-                            acc[h][j][1] += pr * vf[j][1];
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const float4 pr = pr4[i4];
+                        const float prs[4] = {pr.x, pr.y, pr.z, pr.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int i = 4 * i4 + e;
+                            const float w = pb + i < q1 ? prs[e] : 0.0f;
+#pragma unroll
+                            for (int j = 0; j < CPL; ++j) {
+                                acc[h][j][0] += w * vf[i][j][0];
+                                acc[h][j][1] += w * vf[i][j][1];
+                            }
                         }
                     }
                 }
@@ -228,10 +284,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
 
     // Add the four quarters.
 #pragma unroll
-    for (int h = 0; h < kAttnMaxHeads; ++h)
+    for (int h = 0; h < MAXH; ++h)
         if (h < nh)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < CPL; ++j) {
                 const int pp = lane + 64 * j;
                 if (pp < npairs) {
                     red[wq][h][2 * pp] = acc[h][j][0];
@@ -257,20 +313,54 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
 }
 
 // Chunk combine (decode): out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// The first wave forms the chunk weights (n_chunks <= 64); wave w then adds
+// chunks w, w+4, .. for its lanes' dims (loads issued together), and the four
+// partial sums are added in wave order.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
+    __shared__ float wgt[64];
+    __shared__ float inv_l;
+    __shared__ float part[4][kAttnMaxDim];
     const int h = blockIdx.x;
     const int hd = p.head_dim;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float *w = p.ws + (int64_t)h * p.n_chunks * (hd + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < p.n_chunks; ++c) M = fmaxf(M, w[c * (hd + 2) + hd]);
-    float L = 0.0f;
-    for (int c = 0; c < p.n_chunks; ++c)
-        L += expf(w[c * (hd + 2) + hd] - M) * w[c * (hd + 2) + hd + 1];
-    for (int d = threadIdx.x; d < hd; d += 256) {
-        float o = 0.0f;
-        for (int c = 0; c < p.n_chunks; ++c)
-            o += expf(w[c * (hd + 2) + hd] - M) * w[c * (hd + 2) + d];
-        p.out[(int64_t)h * hd + d] = f32_to_f16_bits(L > 0.0f ? o * (1.0f / L) : 0.0f);
+    if (tid < 64) {
+        const bool ok = tid < p.n_chunks;
+        const float m = ok ? w[tid * (hd + 2) + hd] : -INFINITY;
+        const float l = ok ? w[tid * (hd + 2) + hd + 1] : 0.0f;
+        float M = m;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float e = ok ? expf(m - M) : 0.0f;
+        wgt[tid] = e;
+        const float el = e * l;
+        float L = 0.0f;
+        for (int cc = 0; cc < p.n_chunks; ++cc) L += __shfl(el, cc, 64);  // chunk order
+        if (tid == 0) inv_l = L > 0.0f ? 1.0f / L : 0.0f;
+    }
+    __syncthreads();
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float a[16][4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int cc = min(wv + 4 * i, p.n_chunks - 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[i][j] = w[cc * (hd + 2) + min(lane + 64 * j, hd - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int cc = wv + 4 * i;
+        const float e = cc < p.n_chunks ? wgt[cc] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] += e * a[i][j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < hd) part[wv][lane + 64 * j] = o[j];
+    __syncthreads();
+    for (int d = tid; d < hd; d += 256) {
+        const float s = part[0][d] + part[1][d] + part[2][d] + part[3][d];
+        p.out[(int64_t)h * hd + d] = f32_to_f16_bits(s * inv_l);
     }
 }
 
@@ -289,7 +379,9 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
     p.n_kv = n_kv;
     p.head_dim = head_dim;
     p.group = n_heads / n_kv;
-    p.hpw = std::min(p.group, kAttnMaxHeads);
+    // q of the workgroup's heads sits in registers: 8 heads up to 128 dims,
+    // 4 beyond.
+    p.hpw = std::min(p.group, head_dim > 128 ? kAttnMaxHeads / 2 : kAttnMaxHeads);
     p.n_hg = (p.group + p.hpw - 1) / p.hpw;
     p.seq0 = seq0;
     p.scale = scale;
@@ -298,9 +390,9 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
     p.n_chunks = 1;
     p.chunk = seq0 + n_tok;  // whole sequence
     if (n_tok == 1 && seq0 > kAttnTile) {
-        // Decode: split the positions so that about 2 workgroups per CU run.
+        // Decode: split the positions so that about 4 workgroups per CU run.
         const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-        const int want = std::max(1, std::min(64, (2 * cus + units - 1) / units));
+        const int want = std::max(1, std::min(64, (4 * cus + units - 1) / units));
         int chunk = (seq0 + want - 1) / want;
         chunk = (chunk + kAttnTile - 1) / kAttnTile * kAttnTile;
         p.chunk = chunk;
@@ -313,7 +405,18 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
     }
     if (n_tok > 65535) return hipErrorInvalidValue;  // grid.y
     const dim3 grid(units * p.n_chunks, n_tok);
-    attn_kernel<<<grid, 256, 0, st>>>(p);
+    // hpw rounded up to a power of two selects the instance.
+    const int hp2 = p.hpw <= 1 ? 1 : p.hpw <= 2 ? 2 : p.hpw <= 4 ? 4 : 8;
+    if (head_dim > 128) {
+        if (hp2 == 1) attn_kernel<2, 1><<<grid, 256, 0, st>>>(p);
+        else if (hp2 == 2) attn_kernel<2, 2><<<grid, 256, 0, st>>>(p);
+        else attn_kernel<2, 4><<<grid, 256, 0, st>>>(p);
+    } else {
+        if (hp2 == 1) attn_kernel<1, 1><<<grid, 256, 0, st>>>(p);
+        else if (hp2 == 2) attn_kernel<1, 2><<<grid, 256, 0, st>>>(p);
+        else if (hp2 == 4) attn_kernel<1, 4><<<grid, 256, 0, st>>>(p);
+        else attn_kernel<1, 8><<<grid, 256, 0, st>>>(p);
+    }
     if (p.n_chunks > 1) attn_combine_kernel<<<n_heads, 256, 0, st>>>(p);
     return hipGetLastError();
 }
