@@ -21,6 +21,8 @@ stream and timed with HIP events recorded on that stream around replays:
   per_kernel   every decode projection, the LM head [151936 x 2048] fp32
                GEMV, the 4096-id Zipf(1.1) embedding gather, and the prefill
                GEMM at m=512 (TFLOP/s, BASELINE metric's second half)
+  attn_*       decode attention over 4096 positions and causal prefill of 512
+               tokens (32 query / 8 KV heads, head_dim 128, fp16 KV)
   q6k_*        Q6_K (ggml type 14) LM head, embedding gather, down, and the
                mixed Q4_K/Q4_K/Q6_K QKV triple (the Q4_K_M file layout)
   small_batch_decode  m in {1,2,4,8,16} tokens on gate+up and down
@@ -384,6 +386,31 @@ def main() -> int:
         kernels["qkv_q4q4q6_2560x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
                                            "launches": 2}
         del vs6
+
+        # Attention (decode at 4096 positions, prefill of 512 tokens) with
+        # Qwen3-4B-like heads: 32 query heads, 8 KV heads, head_dim 128.
+        AH, AKV, AD = 32, 8, 128
+        caches = [(gen(70_000 + i, (4096, AKV, AD), 1.0).half(), gen(71_000 + i, (4096, AKV, AD), 1.0).half())
+                  for i in range(4)]
+        qa = gen(72_000, (AH * AD,), 1.0).half()
+        oa = torch.empty(AH * AD, dtype=torch.float16, device=dev)
+
+        def attn_launch(i):
+            k, v = caches[i % 4]
+            capi.attention_decode_f16(oa, qa, k, v, AH, AKV, AD, 4096, AD ** -0.5, stream=sp)
+        med, _ = per_launch(attn_launch, 40)
+        b = 2 * 4096 * AKV * AD * 2
+        kernels["attn_decode_fp16_4096"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+        qp = gen(73_000, (512, AH * AD), 1.0).half()
+        op = torch.empty_like(qp)
+
+        def prefill_launch(i):
+            k, v = caches[i % 4]
+            capi.attention_prefill_f16(op, qp, k, v, AH, AKV, AD, 512, 0, AD ** -0.5, stream=sp)
+        med, _ = per_launch(prefill_launch, 8)
+        fl = 4.0 * AH * AD * sum(t + 1 for t in range(512))
+        kernels["attn_prefill_fp16_512"] = {"us": round(med, 3), "TFLOPs": round(fl / med / 1e6, 2)}
+        del caches
 
         # Small-batch decode: m tokens through
         # gemm_quant_batched's C-ABI form with fp16 x / y on the decode
