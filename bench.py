@@ -384,7 +384,7 @@ def main() -> int:
         med, _ = per_launch(mixed_launch, 40)
         b = qbytes(2304, HIDDEN) + q6b(256, HIDDEN) + 2 * HIDDEN + 2 * 2560
         kernels["qkv_q4q4q6_2560x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
-                                           "launches": 2}
+                                           "launches": 1}
         del vs6
 
         # Attention (decode at 4096 positions, prefill of 512 tokens) with

@@ -74,8 +74,8 @@ int rxq4_gemv_f16(void *y, const void *w, int ggml_type, const void *x, int M, i
 int rxq4_gemv_add_f16(void *y, const void *w, int ggml_type, const void *x,
                       const void *residual, int M, int K, void *stream);
 
-/* 1..3 independent GEMVs sharing x; the Q4_K ranges take one launch, each
- * Q5_K / Q6_K range one more.
+/* 1..3 independent GEMVs sharing x, one launch (ranges may mix Q4_K, Q5_K
+ * and Q6_K).
  * Replaces kernels::gemv_quant_pair (reference q4_gemm.cu:2047-2056) with
  * n_ranges = 2 and kernels::gemv_quant_triple (q4_gemm.cu:2058-2069) with 3. */
 int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, int K,

@@ -41,6 +41,10 @@ namespace rxq4 {
 template <int T>
 struct KqFormat;
 template <>
+struct KqFormat<12> {
+    static constexpr int kBytes = 144;
+};
+template <>
 struct KqFormat<13> {
     static constexpr int kBytes = 176;
 };
@@ -210,6 +214,45 @@ __device__ __forceinline__ float q5_slot_dot(const Q5Raw &w, int il, int k0, con
            d * (float)(sc >> 8) * acc_hi - dmin * (float)(mn >> 8) * s_hi;
 }
 
+// ---------------------------------------------------------------- Q4_K slot
+// (only for mixed-type multi-range launches; all-Q4_K work uses gemv_q4k.hip)
+struct Q4Raw {
+    u32x4 hdr, qs0, qs1;
+};
+
+__device__ __forceinline__ void q4_load(__amdgpu_buffer_rsrc_t rs, int boff, int il, Q4Raw &o) {
+    o.hdr = buffer_load16(rs, boff);
+    o.qs0 = buffer_load16(rs, boff + 16 + 32 * il);
+    o.qs1 = buffer_load16(rs, boff + 32 + 32 * il);
+}
+
+__device__ __forceinline__ float q4_slot_dot(const Q4Raw &w, int il, int k0, const XLds &xl) {
+    const float d = f16_bits_to_f32(w.hdr.x & 0xFFFFu);
+    const float dmin = f16_bits_to_f32(w.hdr.x >> 16);
+    uint32_t sc, mn;
+    scale_pair(w.hdr.y, w.hdr.z, w.hdr.w, il, &sc, &mn);
+    const int xl0 = (k0 + 64 * il) >> 3, xh0 = xl0 + 4;
+    const float s_lo = xl.sum[xl0 >> 1] + xl.sum[(xl0 >> 1) + 1];
+    const float s_hi = xl.sum[xh0 >> 1] + xl.sum[(xh0 >> 1) + 1];
+    float acc_lo = -1024.0f * s_lo, acc_hi = -1024.0f * s_hi;
+    const uint32_t qs[8] = {w.qs0.x, w.qs0.y, w.qs0.z, w.qs0.w, w.qs1.x, w.qs1.y, w.qs1.z, w.qs1.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 xlo = xl.x[xl0 + c], xhi = xl.x[xh0 + c];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const uint32_t L = qs[2 * c + h2];
+            const uint32_t qlo = L & 0x0F0F0F0Fu, qhi = (L >> 4) & 0x0F0F0F0Fu;
+            acc_lo = dot2(magic_lo(qlo), xlo[2 * h2], acc_lo);
+            acc_lo = dot2(magic_hi(qlo), xlo[2 * h2 + 1], acc_lo);
+            acc_hi = dot2(magic_lo(qhi), xhi[2 * h2], acc_hi);
+            acc_hi = dot2(magic_hi(qhi), xhi[2 * h2 + 1], acc_hi);
+        }
+    }
+    return d * (float)(sc & 0xFFu) * acc_lo - dmin * (float)(mn & 0xFFu) * s_lo +
+           d * (float)(sc >> 8) * acc_hi - dmin * (float)(mn >> 8) * s_hi;
+}
+
 // ---------------------------------------------------------------- GEMV
 struct KqGemvParams {
     const uint8_t *w;
@@ -224,20 +267,25 @@ struct KqGemvParams {
 
 template <int T>
 struct Slot {
-    using Raw = typename std::conditional<T == 14, Q6Raw, Q5Raw>::type;
+    using Raw = typename std::conditional<
+        T == 14, Q6Raw, typename std::conditional<T == 13, Q5Raw, Q4Raw>::type>::type;
     Raw raw;
     __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int boff, int u) {
         if constexpr (T == 14)
             q6_load(rs, boff, u >> 1, u & 1, raw);
-        else
+        else if constexpr (T == 13)
             q5_load(rs, boff, u, raw);
+        else
+            q4_load(rs, boff, u, raw);
     }
     // k0 = first weight of the block (clamped to a real block for x reads).
     __device__ __forceinline__ float dot(int boff, int u, int k0, const XLds &xl) const {
         if constexpr (T == 14)
             return q6_slot_dot(raw, boff & 3, u >> 1, u & 1, k0, xl);
-        else
+        else if constexpr (T == 13)
             return q5_slot_dot(raw, u, k0, xl);
+        else
+            return q4_slot_dot(raw, u, k0, xl);
     }
 };
 
@@ -329,6 +377,97 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
     }
 }
 
+// Mixed-type multi-range GEMV (pair / triple with a Q5_K or Q6_K range, e.g.
+// the Q4_K q, k + Q6_K v projection): one launch and one x staging for all
+// ranges.  A wave walks units (wave steps or rows) across the ranges; each
+// unit belongs to one range, so its type is uniform and dispatched per unit.
+struct KqMultiRange {
+    const uint8_t *w;
+    uint16_t *y;
+    int type, M, row_bytes, unit0;  // unit0: first global unit of the range
+};
+
+struct KqMultiParams {
+    KqMultiRange r[3];
+    int n_ranges;
+    const uint16_t *x;
+    int K, nb, slots, rows_per, n_units;
+};
+
+template <int T>
+__device__ __forceinline__ void kq_multi_unit(const KqMultiParams &p, const KqMultiRange &r,
+                                              int lu, int lane, const XLds &xl) {
+    constexpr int BYTES = KqFormat<T>::kBytes;
+    if (p.rows_per > 0) {
+        const int sub = lane / p.slots, slot = lane - sub * p.slots;
+        const int r0 = lu * p.rows_per;
+        const int n = min(p.rows_per, r.M - r0);
+        const RowRes rr = row_rsrc(r.w + (int64_t)r0 * r.row_bytes, n * r.row_bytes);
+        const int b = slot >> 2, u = slot & 3;
+        const int boff = rr.ex + sub * r.row_bytes + b * BYTES;
+        Slot<T> S;
+        S.load(rr.rs, boff, u);
+        float v = S.dot(boff, u, b * 256, xl);
+        for (int o = p.slots >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (slot == 0 && sub < n) r.y[r0 + sub] = f32_to_f16_bits(v);
+    } else {
+        const RowRes rr = row_rsrc(r.w + (int64_t)lu * r.row_bytes, r.row_bytes);
+        const int n_iter = (p.slots + 63) >> 6;
+        float v = 0.0f;
+        for (int c = 0; c < n_iter; c += 2) {
+            const int s0 = 64 * c + lane, s1 = s0 + 64;
+            const int b0 = s0 >> 2, b1 = s1 >> 2;
+            const int o0 = rr.ex + b0 * BYTES, o1 = rr.ex + b1 * BYTES;
+            Slot<T> A, B;
+            A.load(rr.rs, o0, s0 & 3);
+            B.load(rr.rs, o1, s1 & 3);
+            v += A.dot(o0, s0 & 3, min(b0, p.nb - 1) * 256, xl);
+            if (c + 1 < n_iter) v += B.dot(o1, s1 & 3, min(b1, p.nb - 1) * 256, xl);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (lane == 0) r.y[lu] = f32_to_f16_bits(v);
+    }
+}
+
+__global__ __launch_bounds__(256) void kq_multi_kernel(KqMultiParams p) {
+    extern __shared__ u32x4 kq_smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    {
+        u32x4 *xs = kq_smem;
+        float *sums = reinterpret_cast<float *>(kq_smem + (p.K >> 3));
+        const u32x4 *xg = reinterpret_cast<const u32x4 *>(p.x);
+        for (int r = tid; r < (p.K >> 4); r += 256) {
+            const u32x4 a = xg[2 * r], b = xg[2 * r + 1];
+            xs[2 * r] = a;
+            xs[2 * r + 1] = b;
+            const uint32_t w8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                s += f16_bits_to_f32(w8[i] & 0xFFFFu);
+                s += f16_bits_to_f32(w8[i] >> 16);
+            }
+            sums[r] = s;
+        }
+    }
+    __syncthreads();
+    const XLds xl{kq_smem, reinterpret_cast<const float *>(kq_smem + (p.K >> 3))};
+    const int n_waves = gridDim.x * 4;
+    for (int u = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(tid >> 6); u < p.n_units;
+         u += n_waves) {
+        const int ri = (p.n_ranges > 1 && u >= p.r[1].unit0) + (p.n_ranges > 2 && u >= p.r[2].unit0);
+        const KqMultiRange &r = p.r[ri];
+        const int lu = u - r.unit0;
+        switch (r.type) {
+            case 12: kq_multi_unit<12>(p, r, lu, lane, xl); break;
+            case 13: kq_multi_unit<13>(p, r, lu, lane, xl); break;
+            default: kq_multi_unit<14>(p, r, lu, lane, xl); break;
+        }
+    }
+}
+
 template <int T, int EPI>
 static hipError_t launch_kq_gemv_t(const KqGemvParams &p, hipStream_t st) {
     const size_t lds = (size_t)p.K * 2 + (size_t)(p.K / 16) * 4;
@@ -378,6 +517,42 @@ hipError_t launch_kq_gemv(int ggml_type, const GemvRange &r, const uint16_t *x, 
     }
 #undef RXQ4_KQ_EPI
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_kq_multi(const GemvRange *ranges, const int *types, int n_ranges,
+                           const uint16_t *x, int K, hipStream_t st) {
+    KqMultiParams p{};
+    p.x = x;
+    p.K = K;
+    p.nb = K / 256;
+    p.slots = 4 * p.nb;
+    p.rows_per = (p.slots <= 64 && 64 % p.slots == 0) ? 64 / p.slots : 0;
+    int units = 0;
+    for (int i = 0; i < n_ranges; ++i) {
+        const int t = types[i];
+        const int bytes = t == 14 ? 210 : t == 13 ? 176 : 144;
+        p.r[p.n_ranges] = KqMultiRange{ranges[i].w, static_cast<uint16_t *>(ranges[i].y), t,
+                                       ranges[i].rows, p.nb * bytes, units};
+        if ((int64_t)(p.rows_per ? p.rows_per : 1) * p.nb * bytes > 0x7FFFFFFF)
+            return hipErrorInvalidValue;
+        units += p.rows_per ? (ranges[i].rows + p.rows_per - 1) / p.rows_per : ranges[i].rows;
+        ++p.n_ranges;
+    }
+    p.n_units = units;
+    if (units == 0) return hipSuccess;
+    const size_t lds = (size_t)K * 2 + (size_t)(K / 16) * 4;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+    const int wg_per_cu = (int)std::max<size_t>(1, std::min<size_t>(4, (160 * 1024) / lds));
+    const int grid = std::max(1, std::min((units + 3) / 4, cus * wg_per_cu));
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_multi_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    kq_multi_kernel<<<grid, 256, lds, st>>>(p);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- embedding

@@ -64,6 +64,10 @@ hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int
 hipError_t launch_kq_gemv(int ggml_type, const GemvRange &r, const uint16_t *x, int K,
                           int epilogue, hipStream_t stream);
 
+// 1..3 ranges of any of Q4_K / Q5_K / Q6_K sharing x, fp16 out, one launch.
+hipError_t launch_kq_multi(const GemvRange *ranges, const int *types, int n_ranges,
+                           const uint16_t *x, int K, hipStream_t stream);
+
 // Q5_K / Q6_K multi-token product for any N >= 1 (16-token chunks).
 hipError_t launch_kq_tokens(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,
                             int x_dtype, int M, int N, int K, hipStream_t stream);

@@ -119,13 +119,14 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
     const char *fn = "rxq4_gemv_multi_f16";
     if (!ranges || n_ranges < 1 || n_ranges > 3)
         return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ranges=%d must be 1..3", fn, n_ranges);
-    // Q4_K ranges share one launch; each Q5_K / Q6_K range is a launch of its
-    // own on the same stream (the reference's mixed Q4/Q4/Q6 triple is one
-    // launch, q4_gemm.cu:1157-1206; the outputs are independent either way).
+    // All-Q4_K ranges take the Q4_K kernels; any Q5_K / Q6_K range makes the
+    // whole call one mixed-type launch (as the reference's mixed Q4/Q4/Q6
+    // triple, q4_gemm.cu:1157-1206).
     rxq4::GemvParams p{};
     rxq4::GemvRange kq[3];
     int kq_type[3];
-    int n_kq = 0;
+    int n_live = 0;
+    bool any_kq = false;
     int64_t total = 0;
     for (int i = 0; i < n_ranges; ++i) {
         const rxq4_rows &r = ranges[i];
@@ -134,35 +135,26 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
         if (r.M < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d M=%d < 0", fn, i, r.M);
         if (r.M > 0 && !r.y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d null y", fn, i);
         const rxq4::GemvRange g{static_cast<const uint8_t *>(r.w), r.y, nullptr, r.M};
-        if (kquant_type(r.ggml_type)) {
-            if (r.M > 0) {
-                kq[n_kq] = g;
-                kq_type[n_kq++] = r.ggml_type;
-            }
-        } else {
-            p.r[p.n_ranges++] = g;
-            total += r.M;
+        any_kq = any_kq || kquant_type(r.ggml_type);
+        if (r.M > 0) {
+            kq[n_live] = g;
+            kq_type[n_live++] = r.ggml_type;
         }
+        p.r[p.n_ranges++] = g;
+        total += r.M;
     }
     int s = check_x(fn, x);
     if (s != RXQ4_STATUS_SUCCESS) return s;
     if (total > 0x7FFFFFFF) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: too many rows", fn);
-    if (total == 0 && n_kq == 0) return ok();
+    if (total == 0) return ok();
     if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const uint16_t *xx = static_cast<const uint16_t *>(x);
-    if (total > 0) {
-        p.total_rows = (int)total;
-        p.x = xx;
-        p.nb = K / 256;
-        hipError_t e = rxq4::launch_gemv(p, rxq4::kEpiF16, st);
-        if (e != hipSuccess) return from_hip(e, fn);
-    }
-    for (int i = 0; i < n_kq; ++i) {
-        hipError_t e = rxq4::launch_kq_gemv(kq_type[i], kq[i], xx, K, rxq4::kEpiF16, st);
-        if (e != hipSuccess) return from_hip(e, fn);
-    }
-    return ok();
+    if (any_kq) return from_hip(rxq4::launch_kq_multi(kq, kq_type, n_live, xx, K, st), fn);
+    p.total_rows = (int)total;
+    p.x = xx;
+    p.nb = K / 256;
+    return from_hip(rxq4::launch_gemv(p, rxq4::kEpiF16, st), fn);
 }
 
 int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x, int x_dtype,

@@ -104,6 +104,30 @@ def test_api_mixed_q4_q4_q6_triple():
         assert util.rounded_ok(host16(yv), orc.kq_gemv_f32(w, K, 13, x16)).all()
 
 
+@pytest.mark.parametrize("K,Ms,types", [
+    (256, (37, 0, 129), (14, 12, 13)),          # 16 rows per wave step, an empty range
+    (11008, (5, 70, 3), (13, 14, 12)),          # long rows
+    (1536, (64, 33, 100), (12, 13, 14)),        # 24 slots per row
+])
+def test_mixed_multi_one_launch(K, Ms, types):
+    """Any mix of Q4_K / Q5_K / Q6_K ranges through gemv_multi (one launch)."""
+    print(f"kq mixed multi K={K} M={Ms} types={types}", flush=True)
+    x16 = util.x_f16(760 + K, K)
+    Wn = [np.zeros(0, np.uint8) if m == 0 else
+          util.weights(761 + i, m, K) if t == 12 else kb.random_blocks(t, util.rng(765 + i), m, K)
+          for i, (m, t) in enumerate(zip(Ms, types))]
+    Wd = [dev(w) if w.size else torch.empty(16, dtype=torch.uint8, device="cuda") for w in Wn]
+    ys = [torch.zeros(max(m, 1), dtype=torch.float16, device="cuda") for m in Ms]
+    x = dev(x16)
+    capi.gemv_multi_f16([(y, w, m, t) for y, w, m, t in zip(ys, Wd, Ms, types)], x, K)
+    for yv, w, m, t in zip(ys, Wn, Ms, types):
+        if m == 0:
+            assert not yv.any()
+            continue
+        ref = orc.kq_gemv_f32(w, K, t, x16)
+        assert util.rounded_ok(host16(yv), ref).all()
+
+
 @pytest.mark.parametrize("K", [256, 2048, 11008])
 def test_q6k_embedding_bit_exact(K):
     V = 40
