@@ -125,14 +125,15 @@ def main() -> int:
         g = torch.Generator(device=dev).manual_seed(seed)
         return torch.randn(shape, generator=g, device=dev) * sigma
 
-    def qweights(seed: int, rows: int, K: int) -> torch.Tensor:
+    def qweights(seed: int, rows: int, K: int, ggml_type: int = 12) -> torch.Tensor:
+        # ggml's reference quantiser (what llama.cpp writes into GGUF files)
         src = gen(seed, (rows, K), 0.02)
-        w = capi.quantize(src)
+        w = capi.quantize_ggml(src, ggml_type)
         del src
         return w
 
     # ------------------------------------------------------------- inputs
-    log("quantising 36 layers of Q4_K weights on the GPU")
+    log("quantising 36 layers of Q4_K weights on the GPU (ggml's reference quantiser)")
     layers = []
     for l in range(N_LAYERS):
         layers.append({
@@ -344,11 +345,7 @@ def main() -> int:
         # Q4_K_M file stores them, and the Qwen3-4B-style mixed QKV triple
         # (Q4_K q, k + Q6_K v).  Random blocks with a fixed d (timing only).
         def q6_blocks(seed, rows, K):
-            g = torch.Generator(device=dev).manual_seed(seed)
-            w = torch.randint(0, 256, (rows, K // 256, 210), generator=g, dtype=torch.uint8,
-                              device=dev)
-            w[:, :, 208], w[:, :, 209] = 0x00, 0x0C  # d = 2^-12
-            return w.reshape(rows, -1)
+            return qweights(seed, rows, K, ggml_type=14)
 
         q6b = lambda rows, K: rows * (K // 256) * 210  # noqa: E731
         heads6 = [q6_blocks(60_000 + i, VOCAB, HIDDEN) for i in range(2)]
@@ -482,7 +479,7 @@ def main() -> int:
         "config": {
             "workload": "decode36: 36 layers x {QKV triple [2048|256|256]x2048, O add "
                         "[2048x2048], gate+up pair [11008|11008]x2048, down add [2048x11008]}, "
-                        "Q4_K N(0,0.02) weights, fp16 N(0,1) activations, M=1, fp32 acc, fp16 out",
+                        "Q4_K weights = ggml reference quantisation of N(0,0.02), fp16 N(0,1) activations, M=1, fp32 acc, fp16 out",
             "launches_per_step": len(calls),
             "bytes_per_step": step_bytes,
             "issue": "eager" if graph is None else "hip_graph",

@@ -110,8 +110,19 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
 int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab,
                         const int32_t *ids, int n_ids, int hidden_dim, void *stream);
 
-/* NEW.  Quantise fp32 rows [n_rows x K] (device) to Q4_K blocks (device). */
+/* NEW.  Quantise fp32 rows [n_rows x K] (device) to Q4_K blocks (device)
+ * with a plain per-sub-block min/max fit (fast; not ggml's search). */
 int rxq4_quantize_q4k(void *dst, const float *src, int64_t n_rows, int K, void *stream);
+
+/* NEW.  Quantise fp32 rows [n_rows x K] (device, 16-byte aligned) to blocks
+ * of ggml_type 12 (Q4_K), 13 (Q5_K) or 14 (Q6_K) (device; 16-byte aligned,
+ * Q6_K 2-byte) with ggml's reference quantisers, byte for byte what
+ * llama.cpp's quantize_row_q{4,5,6}_K_ref write without an importance
+ * matrix (ggml-quants.c), so synthetic weights match real GGUF files
+ * statistically.  No reference counterpart: the reference ships no
+ * quantiser and reads these formats (q4_gemm.cu:147-171). */
+int rxq4_quantize(void *dst, int ggml_type, const float *src, int64_t n_rows, int K,
+                  void *stream);
 
 /* out[n_heads x head_dim] fp16 = attention of one query token over KV
  * positions [0, seq_len): per head h (KV head h / (n_heads / n_kv_heads)),

@@ -52,6 +52,7 @@ def lib() -> ctypes.CDLL:
             "orc_gemv_f64": (None, [P, P, I64, I, P]),
             "orc_gemm_f64": (None, [P, P, I64, I64, I, I, P]),
             "orc_quantize_rows": (None, [P, I64, I, P]),
+            "orc_quantize_ggml": (I, [I, P, I64, I, P]),
             "orc_block_bytes": (I, [I]),
             "orc_kq_dequant_rows_f32": (None, [P, I, I64, I64, I, P]),
             "orc_kq_embed_rows_f16": (None, [P, I, I64, I, P, I64, P]),
@@ -220,6 +221,16 @@ def quantize(src: np.ndarray) -> np.ndarray:
 
 # ---------------------------------------------------------------- Q5_K / Q6_K
 TYPE_BYTES = {12: 144, 13: 176, 14: 210}
+
+
+def quantize_ggml(src: np.ndarray, t: int) -> np.ndarray:
+    """fp32 [rows, K] -> uint8 [rows, K/256 * bytes(t)] with ggml's reference
+    quantiser for type t (12, 13, 14)."""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    rows, K = src.shape
+    out = np.empty((rows, (K // QK_K) * TYPE_BYTES[t]), dtype=np.uint8)
+    assert lib().orc_quantize_ggml(t, _p(src), rows, K, _p(out)) == 0
+    return out
 
 
 def _wt(W, K, t):

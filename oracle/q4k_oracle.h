@@ -118,6 +118,11 @@ void orc_gemm_f64(const void *W, const float *x, int64_t M, int64_t N, int K, in
  * bit for bit. */
 void orc_quantize_rows(const float *src, int64_t n_rows, int K, void *dst);
 
+/* ggml's reference K-quant quantisers (ggml_quant_oracle.c): fp32 rows
+ * [n_rows x K] -> blocks of type 12 (Q4_K), 13 (Q5_K) or 14 (Q6_K).
+ * Returns 0, or -1 for another type or K % 256 != 0. */
+int orc_quantize_ggml(int type, const float *src, int64_t n_rows, int K, void *dst);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,8 +87,12 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
                             int head_dim, int n_tok, int seq0, float scale, int kv_int8,
                             hipStream_t stream);
 
-// fp32 rows -> Q4_K blocks.
+// fp32 rows -> Q4_K blocks (min/max quantiser).
 hipError_t launch_quantize(uint8_t *dst, const float *src, int64_t n_blocks,
                            hipStream_t stream);
+
+// fp32 rows -> blocks of ggml_type 12/13/14 with ggml's reference quantisers.
+hipError_t launch_quantize_ggml(int ggml_type, uint8_t *dst, const float *src, int64_t n_blocks,
+                                hipStream_t stream);
 
 }  // namespace rxq4

@@ -11,12 +11,15 @@
 #include <string.h>
 
 #include "launch.h"
+#include "status.h"
 
 namespace {
-
 thread_local char g_last_error[256] = "";
+}  // namespace
 
-int fail(int status, const char *fmt, ...) {
+namespace rxq4 {
+
+int set_error(int status, const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
@@ -24,14 +27,22 @@ int fail(int status, const char *fmt, ...) {
     return status;
 }
 
-int ok() {
+int set_ok() {
     g_last_error[0] = '\0';
     return RXQ4_STATUS_SUCCESS;
 }
 
+}  // namespace rxq4
+
+namespace {
+
+using rxq4::set_error;
+
+int ok() { return rxq4::set_ok(); }
+
 int from_hip(hipError_t e, const char *what) {
     if (e == hipSuccess) return ok();
-    return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: HIP error %s", what, hipGetErrorString(e));
+    return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: HIP error %s", what, hipGetErrorString(e));
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -41,28 +52,28 @@ bool kquant_type(int t) { return t == RXQ4_GGML_TYPE_Q5_K || t == RXQ4_GGML_TYPE
 // Checks shared by every weight-streaming entry point.
 int check_common(const char *fn, const void *w, int ggml_type, int K) {
     if (ggml_type != RXQ4_GGML_TYPE_Q4_K && !kquant_type(ggml_type))
-        return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT,
+        return set_error(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT,
                     "%s: ggml_type %d not supported (Q4_K = 12, Q5_K = 13, Q6_K = 14)", fn,
                     ggml_type);
     if (K <= 0 || K % 256 != 0 || K > RXQ4_MAX_K)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT,
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT,
                     "%s: K=%d must be a positive multiple of 256 and <= %d", fn, K, RXQ4_MAX_K);
-    if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weight pointer", fn);
+    if (!w) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weight pointer", fn);
     if (!aligned16(w))
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights must be 16-byte aligned", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights must be 16-byte aligned", fn);
     return RXQ4_STATUS_SUCCESS;
 }
 
 // Last check before a launch (the only one that queries the HIP runtime).
 int check_device(const char *fn) {
     if (!rxq4::device_info().arch_ok)
-        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+        return set_error(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
     return RXQ4_STATUS_SUCCESS;
 }
 
 int check_x(const char *fn, const void *x) {
-    if (!x) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null x", fn);
-    if (!aligned16(x)) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: x must be 16-byte aligned", fn);
+    if (!x) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null x", fn);
+    if (!aligned16(x)) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: x must be 16-byte aligned", fn);
     return RXQ4_STATUS_SUCCESS;
 }
 
@@ -71,11 +82,11 @@ int gemv_single(const char *fn, void *y, const void *w, int ggml_type, const voi
     int s = check_common(fn, w, ggml_type, K);
     if (s != RXQ4_STATUS_SUCCESS) return s;
     if ((s = check_x(fn, x)) != RXQ4_STATUS_SUCCESS) return s;
-    if (M < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: M=%d < 0", fn, M);
+    if (M < 0) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: M=%d < 0", fn, M);
     if (M == 0) return ok();
-    if (!y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null y", fn);
+    if (!y) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null y", fn);
     if (epi == rxq4::kEpiAdd && !residual)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null residual", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null residual", fn);
     if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
     const rxq4::GemvRange range{static_cast<const uint8_t *>(w), y,
                                 static_cast<const uint16_t *>(residual), M};
@@ -118,7 +129,7 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
                         void *stream) {
     const char *fn = "rxq4_gemv_multi_f16";
     if (!ranges || n_ranges < 1 || n_ranges > 3)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ranges=%d must be 1..3", fn, n_ranges);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ranges=%d must be 1..3", fn, n_ranges);
     // All-Q4_K ranges take the Q4_K kernels; any Q5_K / Q6_K range makes the
     // whole call one mixed-type launch (as the reference's mixed Q4/Q4/Q6
     // triple, q4_gemm.cu:1157-1206).
@@ -132,8 +143,8 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
         const rxq4_rows &r = ranges[i];
         int s = check_common(fn, r.w, r.ggml_type, K);
         if (s != RXQ4_STATUS_SUCCESS) return s;
-        if (r.M < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d M=%d < 0", fn, i, r.M);
-        if (r.M > 0 && !r.y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d null y", fn, i);
+        if (r.M < 0) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d M=%d < 0", fn, i, r.M);
+        if (r.M > 0 && !r.y) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: range %d null y", fn, i);
         const rxq4::GemvRange g{static_cast<const uint8_t *>(r.w), r.y, nullptr, r.M};
         any_kq = any_kq || kquant_type(r.ggml_type);
         if (r.M > 0) {
@@ -145,7 +156,7 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
     }
     int s = check_x(fn, x);
     if (s != RXQ4_STATUS_SUCCESS) return s;
-    if (total > 0x7FFFFFFF) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: too many rows", fn);
+    if (total > 0x7FFFFFFF) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: too many rows", fn);
     if (total == 0) return ok();
     if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -163,15 +174,15 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
     int s = check_common(fn, w, ggml_type, K);
     if (s != RXQ4_STATUS_SUCCESS) return s;
     if ((s = check_x(fn, x)) != RXQ4_STATUS_SUCCESS) return s;
-    if (M < 0 || N < 0) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: M=%d N=%d", fn, M, N);
+    if (M < 0 || N < 0) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: M=%d N=%d", fn, M, N);
     if (M == 0 || N == 0) return ok();
-    if (!y) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null y", fn);
+    if (!y) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null y", fn);
     const bool f16_ok = x_dtype == RXQ4_DTYPE_F16 &&
                         (y_dtype == RXQ4_DTYPE_F16 || y_dtype == RXQ4_DTYPE_F32);
     const bool bf16_ok = x_dtype == RXQ4_DTYPE_BF16 &&
                          (y_dtype == RXQ4_DTYPE_BF16 || y_dtype == RXQ4_DTYPE_F32);
     if (!f16_ok && !bf16_ok)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: unsupported dtypes x=%d y=%d", fn,
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: unsupported dtypes x=%d y=%d", fn,
                     x_dtype, y_dtype);
     if ((s = check_device(fn)) != RXQ4_STATUS_SUCCESS) return s;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -204,15 +215,15 @@ int rxq4_embed_row_f16(void *dst, const void *w, int ggml_type, int token_id, in
     // Order of checks as the reference (q4_gemm.cu:2079-2105): shape first,
     // then the weight pointer, then the type.
     if (hidden_dim <= 0 || hidden_dim % 256 != 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
-    if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
+    if (!w) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
     // Q4_K and Q6_K, as the reference (q4_gemm.cu:2089-2106).
     if (ggml_type != RXQ4_GGML_TYPE_Q4_K && ggml_type != RXQ4_GGML_TYPE_Q6_K)
-        return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
+        return set_error(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
     if (!aligned16(w) || !dst || !aligned16(dst))
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights/dst must be 16-byte aligned", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights/dst must be 16-byte aligned", fn);
     if (!rxq4::device_info().arch_ok)
-        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+        return set_error(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
     const auto launch = ggml_type == RXQ4_GGML_TYPE_Q6_K ? rxq4::launch_kq_embed : rxq4::launch_embed;
     return from_hip(launch(static_cast<uint16_t *>(dst), static_cast<const uint8_t *>(w), nullptr,
                            token_id, 0, 1, hidden_dim, static_cast<hipStream_t>(stream)),
@@ -223,18 +234,18 @@ int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab
                         const int32_t *ids, int n_ids, int hidden_dim, void *stream) {
     const char *fn = "rxq4_embed_rows_f16";
     if (hidden_dim <= 0 || hidden_dim % 256 != 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
-    if (!w) return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: hidden_dim=%d", fn, hidden_dim);
+    if (!w) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weights", fn);
     if (ggml_type != RXQ4_GGML_TYPE_Q4_K && ggml_type != RXQ4_GGML_TYPE_Q6_K)
-        return fail(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
+        return set_error(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
     if (n_ids < 0 || n_vocab < 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ids=%d n_vocab=%lld", fn, n_ids,
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ids=%d n_vocab=%lld", fn, n_ids,
                     (long long)n_vocab);
     if (n_ids == 0) return ok();
     if (!ids || !dst || !aligned16(w) || !aligned16(dst))
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
     if (!rxq4::device_info().arch_ok)
-        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+        return set_error(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
     const auto launch = ggml_type == RXQ4_GGML_TYPE_Q6_K ? rxq4::launch_kq_embed : rxq4::launch_embed;
     return from_hip(launch(static_cast<uint16_t *>(dst), static_cast<const uint8_t *>(w), ids, 0,
                            n_vocab, n_ids, hidden_dim, static_cast<hipStream_t>(stream)),
@@ -244,15 +255,41 @@ int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab
 int rxq4_quantize_q4k(void *dst, const float *src, int64_t n_rows, int K, void *stream) {
     const char *fn = "rxq4_quantize_q4k";
     if (K <= 0 || K % 256 != 0 || n_rows < 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: K=%d n_rows=%lld", fn, K,
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: K=%d n_rows=%lld", fn, K,
                     (long long)n_rows);
     if (n_rows == 0) return ok();
     if (!dst || !src || !aligned16(dst) || !aligned16(src))
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
     if (!rxq4::device_info().arch_ok)
-        return fail(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+        return set_error(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
     return from_hip(rxq4::launch_quantize(static_cast<uint8_t *>(dst), src, n_rows * (K / 256),
                                           static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int rxq4_quantize(void *dst, int ggml_type, const float *src, int64_t n_rows, int K,
+                  void *stream) {
+    const char *fn = "rxq4_quantize";
+    if (ggml_type != RXQ4_GGML_TYPE_Q4_K && !kquant_type(ggml_type))
+        return set_error(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT,
+                         "%s: ggml_type %d not supported (Q4_K = 12, Q5_K = 13, Q6_K = 14)", fn,
+                         ggml_type);
+    if (K <= 0 || K % 256 != 0 || n_rows < 0)
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: K=%d n_rows=%lld", fn, K,
+                         (long long)n_rows);
+    if (n_rows == 0) return ok();
+    if (!dst || !src || !aligned16(src))
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null or misaligned src", fn);
+    const uintptr_t need = ggml_type == RXQ4_GGML_TYPE_Q6_K ? 1u : 15u;
+    if ((reinterpret_cast<uintptr_t>(dst) & need) != 0)
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: dst must be %d-byte aligned", fn,
+                         (int)need + 1);
+    if (n_rows > INT64_MAX / (K / 256))
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: too many rows", fn);
+    if (!rxq4::device_info().arch_ok)
+        return set_error(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
+    return from_hip(rxq4::launch_quantize_ggml(ggml_type, static_cast<uint8_t *>(dst), src,
+                                               n_rows * (K / 256), static_cast<hipStream_t>(stream)),
                     fn);
 }
 
@@ -265,19 +302,19 @@ int attention(const char *fn, void *out, const void *q, const void *k, const voi
               const float *ks, const float *vs, void *stream) {
     if (n_heads == 0 || n_tok == 0) return ok();
     if (n_heads < 0 || n_kv <= 0 || n_heads % n_kv != 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT,
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT,
                     "%s: n_heads=%d must be a positive multiple of n_kv_heads=%d", fn, n_heads,
                     n_kv);
     const int align = kv_int8 ? 16 : 8;
     if (head_dim <= 0 || head_dim > 256 || head_dim % align != 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT,
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT,
                     "%s: head_dim=%d must be a multiple of %d and <= 256", fn, head_dim, align);
     if (n_tok < 0 || seq0 < 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: negative length", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: negative length", fn);
     if (!out || !q || !aligned16(out) || !aligned16(q))
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: q/out null or not 16-byte aligned", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: q/out null or not 16-byte aligned", fn);
     if (seq0 + n_tok - 1 > 0 && (!k || !v || !aligned16(k) || !aligned16(v)))
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "%s: k/v null or not 16-byte aligned", fn);
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: k/v null or not 16-byte aligned", fn);
     int s = check_device(fn);
     if (s != RXQ4_STATUS_SUCCESS) return s;
     return from_hip(rxq4::launch_attention(static_cast<uint16_t *>(out),
@@ -297,7 +334,7 @@ int rxq4_attention_decode_f16(void *out, const void *q, const void *k_cache,
                               int seq_len, float scale, int kv_int8, const float *k_scales,
                               const float *v_scales, void *stream) {
     if (seq_len < 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "rxq4_attention_decode_f16: seq_len=%d",
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "rxq4_attention_decode_f16: seq_len=%d",
                     seq_len);
     return attention("rxq4_attention_decode_f16", out, q, k_cache, v_cache, n_heads, n_kv_heads,
                      head_dim, 1, seq_len, scale, kv_int8, k_scales, v_scales, stream);
@@ -308,7 +345,7 @@ int rxq4_attention_prefill_f16(void *out, const void *q, const void *k_cache,
                                int N, int start_pos, float scale, int kv_int8,
                                const float *k_scales, const float *v_scales, void *stream) {
     if (N < 0 || start_pos < 0)
-        return fail(RXQ4_STATUS_INVALID_ARGUMENT, "rxq4_attention_prefill_f16: N=%d start_pos=%d",
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "rxq4_attention_prefill_f16: N=%d start_pos=%d",
                     N, start_pos);
     return attention("rxq4_attention_prefill_f16", out, q, k_cache, v_cache, n_heads, n_kv_heads,
                      head_dim, N, start_pos + 1, scale, kv_int8, k_scales, v_scales, stream);

@@ -35,6 +35,7 @@ SIGNATURES = {
     "rxq4_embed_rows_f16": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int, c_int,
                                     c_void_p]),
     "rxq4_quantize_q4k": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p]),
+    "rxq4_quantize": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p]),
     "rxq4_attention_decode_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                           c_int, c_int, ctypes.c_float, c_int, c_void_p,
                                           c_void_p, c_void_p]),
@@ -148,6 +149,20 @@ def quantize(src: torch.Tensor, stream=None) -> torch.Tensor:
     rows, K = src.shape
     dst = torch.empty((rows, (K // 256) * 144), dtype=torch.uint8, device=src.device)
     quantize_q4k(dst, src.contiguous(), rows, K, stream)
+    return dst
+
+
+_TYPE_BYTES = {12: 144, 13: 176, 14: 210}
+
+
+def quantize_ggml(src: torch.Tensor, ggml_type: int = GGML_TYPE_Q4_K, stream=None) -> torch.Tensor:
+    """ggml's reference quantiser on the GPU: device fp32 [rows, K] -> uint8
+    [rows, K/256 * block bytes] of ggml_type 12, 13 or 14."""
+    rows, K = src.shape
+    dst = torch.empty((rows, (K // 256) * _TYPE_BYTES.get(ggml_type, 144)), dtype=torch.uint8,
+                      device=src.device)
+    _check(lib().rxq4_quantize(_ptr(dst), ggml_type, _ptr(src.contiguous()), rows, K,
+                               _stream(stream)), "rxq4_quantize")
     return dst
 
 

@@ -5,7 +5,8 @@
   * the library defines every public symbol the reference's dispatcher
     defines and every kernel-seam symbol it needs
     (reference src/dispatch.cpp, src/kernels/kernel_entrypoints.h:7-16);
-  * the library exports every entry point declared in include/rxq4.h;
+  * the library exports every entry point declared in include/rxq4.h and
+    include/rxq4_gguf.h;
   * the reference's own dispatcher (src/dispatch.cpp compiled from its
     sources) links against the kernels-only library and its calls land in
     this build's seam (statuses the seam returns before any GPU work).
@@ -87,9 +88,10 @@ def test_reference_dispatcher_runs_on_this_kernel_layer():
                    "flash_attention_decode": 0, "registry_empty": 1}
 
 
-def test_library_exports_every_c_abi_entry_point():
-    header = open(os.path.join(ROOT, "include", "rxq4.h")).read()
-    names = set(re.findall(r"\b(rxq4_[a-z0-9_]+)\s*\(", header))
+@pytest.mark.parametrize("header", ["rxq4.h", "rxq4_gguf.h"])
+def test_library_exports_every_c_abi_entry_point(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    names = set(re.findall(r"\b(rxq4_[a-z0-9_]+)\s*\(", text))
     assert len(names) >= 12
     lib = ctypes.CDLL(LIB)
     for n in sorted(names):
