@@ -105,8 +105,11 @@ def test_gpu_quantizer_matches_oracle(rows, K):
 
 
 # ---------------------------------------------------------------------- GEMV
+# register kernel (slots | 64), LDS kernel (other K: 2816, 1536, 5632, 11008,
+# 16384, 65536)
 SHAPES = [(2048, 2048), (7, 256), (33, 512), (2560, 2048), (301, 4096), (64, 11008),
-          (50, 2816), (3, 65536), (129, 1024)]
+          (50, 2816), (3, 65536), (129, 1024), (70, 1536), (45, 5632), (20, 16384),
+          (2051, 11008)]
 
 
 @pytest.mark.parametrize("M,K", SHAPES)
@@ -191,6 +194,19 @@ def test_api_pair_and_triple_match_single_gemvs():
     for yv, w in zip(ys, Wn):
         ref = orc.gemv_f32(w, K, x16)
         assert util.rounded_ok(host16(yv), ref).all()
+
+
+def test_pair_on_long_rows():
+    """A pair whose rows take the LDS kernel (long rows)."""
+    K = 11008
+    x16 = util.x_f16(75, K)
+    x = dev(x16)
+    Ws = [util.weights(76, 13, K), util.weights(77, 30, K)]
+    ys = [torch.empty(w.shape[0], dtype=torch.float16, device="cuda") for w in Ws]
+    Wd = [dev(w) for w in Ws]
+    capi.gemv_multi_f16([(ys[0], Wd[0], 13), (ys[1], Wd[1], 30)], x, K)
+    for yv, Wn in zip(ys, Ws):
+        assert util.rounded_ok(host16(yv), orc.gemv_f32(Wn, K, x16)).all()
 
 
 def test_api_gemv_pointer_resolution():
