@@ -23,10 +23,12 @@
 // writes (max, sum, unnormalised output) to a workspace and a second launch
 // combines the chunks in chunk order (results do not depend on scheduling).
 #include <math.h>
+#include <stdlib.h>
 
 #include <algorithm>
 
 #include "launch.h"
+#include "mfma_util.h"
 #include "q4k_device.h"
 
 namespace rxq4 {
@@ -411,6 +413,237 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill on the matrix cores (head_dim 64 or 128).  A workgroup takes one
+// KV head, HB of its query heads and TPB = 4 * (16 / HB) consecutive tokens;
+// wave w owns 16 "query rows" (token, head) = (16 / HB tokens) x (HB heads),
+// all sharing the KV head, so K/V tiles are read once per workgroup.
+// Per 64-position tile, staged in LDS (K row-major, V transposed) with the
+// next tile's global loads in flight during this tile's arithmetic:
+//   S^T = K . Q^T   v_mfma_f32_16x16x32_f16: src0 = 16 positions x 32 dims
+//                   of K (LDS), src1 = Q^T (registers); lane l ends up with
+//                   positions 4 (l/16) + i of query row l % 16;
+//   online softmax  per query row (lane l % 16): the four lane groups
+//                   combine with two shuffles; exp2 of log2e-scaled scores;
+//   O^T += V^T . P^T the same MFMA with src0 = 16 dims x 32 positions of V^T
+//                   (LDS) and src1 = P^T straight from the score registers
+//                   (the k order of a lane group is its positions
+//                   {4g + i, 16 + 4g + i}, in both operands).  P is split
+//                   into fp16 hi + lo parts (two MFMAs), so the products
+//                   keep ~22 bits of the fp32 probabilities.
+// Causal: query row (t, h) sees positions [0, start + t]; rows of a tile
+// past that get probability 0 (rows with nothing visible yet keep m = -inf).
+template <int HD, int HB, bool I8>
+__global__ __launch_bounds__(256) void attn_prefill_mfma(AttnParams p, int start, int n_tok) {
+    constexpr int TPW = 16 / HB;       // tokens per wave
+    constexpr int TPB = 4 * TPW;       // tokens per workgroup
+    constexpr int KROW = HD + 8;       // LDS K row (fp16), padded
+    constexpr int VROW = kAttnTile + 4;  // LDS V^T row (fp16), padded
+    constexpr int KCH = HD / 8;        // 8-dim chunks per row
+    constexpr int NST = kAttnTile * KCH / 256;  // staged chunks per thread (K and V each)
+    __shared__ __attribute__((aligned(16))) uint16_t kt[2][kAttnTile * KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * VROW];
+    __shared__ float ksc[2][kAttnTile], vsc[2][kAttnTile];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int n_tb = (n_tok + TPB - 1) / TPB;
+    const int tb = n_tb - 1 - (int)(blockIdx.x % n_tb);  // longest rows first
+    const int hbk = blockIdx.x / n_tb;
+    const int n_hb = p.group / HB;
+    const int kvh = hbk / n_hb;
+    const int h = kvh * p.group + (hbk % n_hb) * HB + (r % HB);
+    const int t = tb * TPB + w * TPW + r / HB;
+    const bool row_ok = t < n_tok;
+    const int tc = row_ok ? t : n_tok - 1;
+    const int qpos = start + tc;  // last visible position of this query row
+    const int pos_end = start + min(n_tok, (tb + 1) * TPB);
+    const int n_tiles = (pos_end + kAttnTile - 1) / kAttnTile;
+    constexpr int esz = I8 ? 1 : 2;
+    const int64_t row_stride = (int64_t)p.n_kv * HD * esz;
+    const uint8_t *kb = static_cast<const uint8_t *>(p.k) + (int64_t)kvh * HD * esz;
+    const uint8_t *vb = static_cast<const uint8_t *>(p.v) + (int64_t)kvh * HD * esz;
+    const float *ksp = p.ks ? p.ks + kvh : &g_attn_one;
+    const float *vsp = p.vs ? p.vs + kvh : &g_attn_one;
+    const int s_stride = p.ks ? p.n_kv : 0, v_stride = p.vs ? p.n_kv : 0;
+
+    // Q^T fragments: dims 32 ks + 8 g .. + 8 of query row r.
+    u32x4 qf[HD / 32];
+    {
+        const uint16_t *qrow = p.q + ((int64_t)tc * p.n_heads + h) * HD;
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ++ks)
+            qf[ks] = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks + 8 * g);
+    }
+
+    // Staging registers: K chunks row-major (16 lanes per row: coalesced),
+    // V chunks position-major (consecutive lanes, consecutive positions: the
+    // transposed LDS writes do not collide).
+    u32x4 kr[NST], vr[NST];
+    float ksr = 1.0f, vsr = 1.0f;
+    auto load_tile = [&](int p0) {
+#pragma unroll
+        for (int j = 0; j < NST; ++j) {
+            const int id = tid + 256 * j;
+            const int kpos = min(p0 + id / KCH, pos_end - 1), kc = id % KCH;
+            const int vpos = min(p0 + id % kAttnTile, pos_end - 1), vc = id / kAttnTile;
+            const uint8_t *krow = kb + kpos * row_stride;
+            const uint8_t *vrow = vb + vpos * row_stride;
+            if (I8) {
+                const u32x2 a = reinterpret_cast<const u32x2 *>(krow)[kc];
+                const u32x2 b = reinterpret_cast<const u32x2 *>(vrow)[vc];
+                kr[j] = u32x4{a.x, a.y, 0u, 0u};
+                vr[j] = u32x4{b.x, b.y, 0u, 0u};
+            } else {
+                kr[j] = reinterpret_cast<const u32x4 *>(krow)[kc];
+                vr[j] = reinterpret_cast<const u32x4 *>(vrow)[vc];
+            }
+        }
+        if (I8 && tid < kAttnTile) {
+            const int pos = min(p0 + tid, pos_end - 1);
+            ksr = ksp[(int64_t)pos * s_stride];
+            vsr = vsp[(int64_t)pos * v_stride];
+        }
+    };
+    // 8 int8 (bytes of .x, .y) as 8 fp16 (exact).
+    auto i8_to_f16 = [](u32x4 v) {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t wd = e < 2 ? v.x : v.y;
+            const int sh = 16 * (e & 1);
+            o[e] = pack2<RXQ4_DTYPE_F16>((float)(int8_t)(uint8_t)(wd >> sh),
+                                         (float)(int8_t)(uint8_t)(wd >> (sh + 8)));
+        }
+        return u32x4{o[0], o[1], o[2], o[3]};
+    };
+    auto store_tile = [&](int b) {
+#pragma unroll
+        for (int j = 0; j < NST; ++j) {
+            const int id = tid + 256 * j;
+            const u32x4 kv = I8 ? i8_to_f16(kr[j]) : kr[j];
+            *reinterpret_cast<u32x4 *>(&kt[b][(id / KCH) * KROW + 8 * (id % KCH)]) = kv;
+            const u32x4 vv = I8 ? i8_to_f16(vr[j]) : vr[j];
+            const uint32_t wv[4] = {vv.x, vv.y, vv.z, vv.w};
+            const int vpos = id % kAttnTile, d0 = 8 * (id / kAttnTile);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                vt[b][(d0 + e) * VROW + vpos] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+        }
+        if (I8 && tid < kAttnTile) {
+            ksc[b][tid] = ksr;
+            vsc[b][tid] = vsr;
+        }
+    };
+
+    f32x4 o[HD / 16];
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    const float sl2 = p.scale * 1.4426950408889634f;  // scores in log2 units
+
+    load_tile(0);
+    store_tile(0);
+    lds_sync();
+    for (int it = 0; it < n_tiles; ++it) {
+        const int b = it & 1, p0 = it * kAttnTile;
+        load_tile(p0 + kAttnTile);  // past the end: clamped re-reads, not stored
+        // S^T for the 4 sub-tiles of 16 positions.
+        float sv[4][4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < HD / 32; ++ks) {
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(
+                    &kt[b][(16 * st + r) * KROW + 32 * ks + 8 * g]);
+                acc = mfma<RXQ4_DTYPE_F16>(a, qf[ks], acc);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int pp = 16 * st + 4 * g + i;
+                const float s = acc[i] * sl2 * (I8 ? ksc[b][pp] : 1.0f);
+                sv[st][i] = p0 + pp <= qpos ? s : -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[st][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);
+        const bool live = m_new != -INFINITY;  // something visible so far
+        const float corr = live ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+        float sum = 0.0f;
+        uint32_t ph[2][4], pl[2][4];  // P^T hi / lo operands per 32-position k step
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                float e0 = live && sv[st][i] != -INFINITY ? __builtin_amdgcn_exp2f(sv[st][i] - m_new) : 0.0f;
+                float e1 = live && sv[st][i + 1] != -INFINITY ? __builtin_amdgcn_exp2f(sv[st][i + 1] - m_new) : 0.0f;
+                sum += e0;
+                sum += e1;
+                if (I8) {
+                    e0 *= vsc[b][16 * st + 4 * g + i];
+                    e1 *= vsc[b][16 * st + 4 * g + i + 1];
+                }
+                const uint32_t hi = pack2<RXQ4_DTYPE_F16>(e0, e1);
+                const f16x2 hv = __builtin_bit_cast(f16x2, hi);
+                const uint32_t lo = pack2<RXQ4_DTYPE_F16>(e0 - (float)hv[0], e1 - (float)hv[1]);
+                // k order of lane group g in step ks2: sub-tile 2 ks2 then 2 ks2 + 1
+                ph[st >> 1][2 * (st & 1) + (i >> 1)] = hi;
+                pl[st >> 1][2 * (st & 1) + (i >> 1)] = lo;
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        l = l * corr + sum;
+        m = m_new;
+        // O^T = corr * O^T + V^T . P^T
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) {
+            o[dt] *= corr;
+#pragma unroll
+            for (int ks2 = 0; ks2 < 2; ++ks2) {
+                const uint16_t *vrow = &vt[b][(16 * dt + r) * VROW + 32 * ks2 + 4 * g];
+                const u32x2 v0 = *reinterpret_cast<const u32x2 *>(vrow);
+                const u32x2 v1 = *reinterpret_cast<const u32x2 *>(vrow + 16);
+                const u32x4 a = u32x4{v0.x, v0.y, v1.x, v1.y};
+                o[dt] = mfma<RXQ4_DTYPE_F16>(a, u32x4{ph[ks2][0], ph[ks2][1], ph[ks2][2], ph[ks2][3]}, o[dt]);
+                o[dt] = mfma<RXQ4_DTYPE_F16>(a, u32x4{pl[ks2][0], pl[ks2][1], pl[ks2][2], pl[ks2][3]}, o[dt]);
+            }
+        }
+        if (it + 1 < n_tiles) store_tile(b ^ 1);  // uniform
+        lds_sync();
+    }
+    if (row_ok) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        uint16_t *orow = p.out + ((int64_t)t * p.n_heads + h) * HD;
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) {
+            const uint32_t a = pack2<RXQ4_DTYPE_F16>(o[dt][0] * inv, o[dt][1] * inv);
+            const uint32_t c = pack2<RXQ4_DTYPE_F16>(o[dt][2] * inv, o[dt][3] * inv);
+            *reinterpret_cast<u32x2 *>(orow + 16 * dt + 4 * g) = u32x2{a, c};
+        }
+    }
+}
+
+template <int HD, bool I8>
+static void launch_prefill_hd(const AttnParams &p, int hb, int start, int n_tok, hipStream_t st) {
+    const int units = p.n_kv * (p.group / hb);
+    const int tpb = 4 * (16 / hb);
+    const unsigned grid = (unsigned)(units * ((n_tok + tpb - 1) / tpb));
+    switch (hb) {
+        case 1: attn_prefill_mfma<HD, 1, I8><<<grid, 256, 0, st>>>(p, start, n_tok); break;
+        case 2: attn_prefill_mfma<HD, 2, I8><<<grid, 256, 0, st>>>(p, start, n_tok); break;
+        case 4: attn_prefill_mfma<HD, 4, I8><<<grid, 256, 0, st>>>(p, start, n_tok); break;
+        case 8: attn_prefill_mfma<HD, 8, I8><<<grid, 256, 0, st>>>(p, start, n_tok); break;
+        default: attn_prefill_mfma<HD, 16, I8><<<grid, 256, 0, st>>>(p, start, n_tok); break;
+    }
+}
+
 template <bool I8>
 static void launch_attn_t(const AttnParams &p, dim3 grid, int hp2, bool wide, hipStream_t st) {
     if (wide) {
@@ -423,6 +656,12 @@ static void launch_attn_t(const AttnParams &p, dim3 grid, int hp2, bool wide, hi
         else if (hp2 == 4) attn_kernel<1, 4, I8><<<grid, 256, 0, st>>>(p);
         else attn_kernel<1, 8, I8><<<grid, 256, 0, st>>>(p);
     }
+}
+
+// RXQ4_ATTN_MFMA=0 keeps prefill on the VALU kernel (for comparisons).
+static bool env_attn_mfma() {
+    const char *v = getenv("RXQ4_ATTN_MFMA");
+    return !(v && v[0] == '0');
 }
 
 hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, const void *v,
@@ -463,6 +702,23 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
             const hipError_t e = device_workspace(bytes, &p.ws);
             if (e != hipSuccess) return e;
         }
+    }
+    if (n_tok > 1 && (head_dim == 64 || head_dim == 128) && env_attn_mfma()) {
+        // Prefill on the matrix cores; HB = the largest power of two <= 16
+        // dividing the GQA group.
+        int hb = 1;
+        while (hb < 16 && p.group % (2 * hb) == 0) hb *= 2;
+        const int start = seq0 - 1;
+        const int64_t blocks = (int64_t)n_kv * (p.group / hb) * ((n_tok + 4 * (16 / hb) - 1) / (4 * (16 / hb)));
+        if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+        if (head_dim == 64) {
+            if (kv_int8) launch_prefill_hd<64, true>(p, hb, start, n_tok, st);
+            else launch_prefill_hd<64, false>(p, hb, start, n_tok, st);
+        } else {
+            if (kv_int8) launch_prefill_hd<128, true>(p, hb, start, n_tok, st);
+            else launch_prefill_hd<128, false>(p, hb, start, n_tok, st);
+        }
+        return hipGetLastError();
     }
     if (n_tok > 65535) return hipErrorInvalidValue;  // grid.y
     const dim3 grid(units * p.n_chunks, n_tok);

@@ -119,3 +119,41 @@ def test_decode_api_matches_c_abi():
                                 seq_len=S, scale=0.088)
     assert api.call("flash_attention_decode", a) == rxq4.SUCCESS
     assert torch.equal(o1, o2)
+
+
+# (n_heads, n_kv, head_dim, N, start_pos, int8): GQA groups 1, 2 (6 heads per
+# KV head: two head blocks), 4, 8 and 32 (two blocks of 16), head_dim 64 and
+# 128 (matrix-core prefill) and 80 (VALU kernel), N not a multiple of the
+# token block, int8 with and without scales.
+PREFILL = [(32, 8, 128, 100, 0, False), (16, 4, 128, 300, 37, False), (8, 8, 64, 70, 5, False),
+           (16, 2, 64, 33, 200, False), (32, 1, 128, 20, 10, False), (12, 2, 128, 17, 3, False),
+           (16, 4, 128, 50, 64, "scales"), (8, 2, 64, 40, 0, "plain"), (4, 2, 80, 9, 4, False)]
+
+
+@pytest.mark.parametrize("H,KV,D,N,start,i8", PREFILL)
+def test_prefill_shapes(H, KV, D, N, start, i8):
+    print(f"attention prefill H={H} KV={KV} D={D} N={N} start={start} int8={i8}", flush=True)
+    S = start + N
+    r = util.rng(940 + N + D)
+    q = f16(r.standard_normal((N, H * D)))
+    if i8:
+        k = r.integers(-127, 128, (S, KV, D)).astype(np.int8)
+        v = r.integers(-127, 128, (S, KV, D)).astype(np.int8)
+        ks = (r.random((S, KV)) * 0.02 + 0.001).astype(np.float32) if i8 == "scales" else None
+        vs = (r.random((S, KV)) * 0.02 + 0.001).astype(np.float32) if i8 == "scales" else None
+        scale = 1.0 / np.sqrt(D) if i8 == "scales" else 0.002
+        kd, vd = torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+    else:
+        k = f16(r.standard_normal((S, KV, D)))
+        v = f16(r.standard_normal((S, KV, D)))
+        ks = vs = None
+        scale = 1.0 / np.sqrt(D)
+        kd, vd = dev16(k), dev16(v)
+    t = lambda a: None if a is None else torch.from_numpy(a).cuda()  # noqa: E731
+    out = torch.empty((N, H * D), dtype=torch.float16, device="cuda")
+    capi.attention_prefill_f16(out, dev16(q), kd, vd, H, KV, D, N, start, scale, bool(i8), t(ks), t(vs))
+    got = host16(out).reshape(N, -1)
+    ref32 = orc.attn_prefill_f32(q, k, v, H, KV, D, N, start, scale, bool(i8), ks, vs).reshape(N, -1)
+    for tk in range(N):
+        ref64 = orc.attn_decode_f64(q[tk], k, v, H, KV, D, start + tk + 1, scale, bool(i8), ks, vs)
+        check(got[tk], ref64, ref32[tk])
