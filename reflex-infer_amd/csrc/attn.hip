@@ -171,11 +171,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
         }
     };
 
-    KvTile<CPL, I8> A, B;
-    load_tile(beg, A);
-
-    // q of the group's heads (16-byte loads, clamped; zero past the group).
+    // q of the group's heads (16-byte loads, clamped; zero past the group),
+    // issued ahead of the first tile so that it lands first.
     float qr[CPL][MAXH][8];
+    KvTile<CPL, I8> A, B;
     {
         u32x4 qraw[CPL][MAXH];
 #pragma unroll
@@ -187,6 +186,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
                 qraw[j][h] = *reinterpret_cast<const u32x4 *>(
                     p.q + t * q_dim + (int64_t)(h0 + hh) * hd + 8 * ch);
             }
+        load_tile(beg, A);
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
 #pragma unroll
@@ -319,15 +319,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
 
     // Two tiles in flight: the next tile's loads go out before this tile's
     // arithmetic (the one past the end re-reads the last row: cache hits).
-    for (int p0 = beg;;) {
-        load_tile(p0 + kAttnTile, B);
-        process(p0, A, 0);
-        p0 += kAttnTile;
-        if (p0 >= end) break;
-        load_tile(p0 + kAttnTile, A);
-        process(p0, B, 1);
-        p0 += kAttnTile;
-        if (p0 >= end) break;
+    // A chunk of one tile (most decode splits) has nothing to prefetch.
+    if (end - beg <= kAttnTile) {
+        process(beg, A, 0);
+    } else {
+        for (int p0 = beg;;) {
+            load_tile(p0 + kAttnTile, B);
+            process(p0, A, 0);
+            p0 += kAttnTile;
+            if (p0 >= end) break;
+            load_tile(p0 + kAttnTile, A);
+            process(p0, B, 1);
+            p0 += kAttnTile;
+            if (p0 >= end) break;
+        }
     }
 
     // Add the four quarters.
@@ -363,8 +368,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
 // Chunk combine (decode): out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
 // Workgroup (head, 64-dim slice); every load is issued before the barrier:
 // the first wave's chunk statistics and each wave's chunks w, w+4, .. for its
-// lane's dim.  The first wave forms the weights; the four partial sums are
-// added in wave order (results do not depend on scheduling).
+// lane's dim.  The first wave forms the weights; all sums use fixed orders
+// (a butterfly for the denominator, chunks w, w+4, .. per wave, then the
+// waves in order), so results do not depend on scheduling.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     __shared__ float wgt[64];
     __shared__ float inv_l;
@@ -393,9 +399,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
         for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
         const float e = ok ? expf(m - M) : 0.0f;
         wgt[lane] = e;
-        const float el = ok ? e * l : 0.0f;
-        float L = 0.0f;
-        for (int cc = 0; cc < p.n_chunks; ++cc) L += __shfl(el, cc, 64);  // chunk order
+        // Butterfly sum: a fixed association (every lane gets the same
+        // value), so the result does not depend on scheduling.
+        float L = ok ? e * l : 0.0f;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) L += __shfl_xor(L, o, 64);
         if (lane == 0) inv_l = L > 0.0f ? 1.0f / L : 0.0f;
     }
     lds_sync();
@@ -692,7 +700,9 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
     if (n_tok == 1 && seq0 > kAttnTile) {
         // Decode: split the positions so that about 4 workgroups per CU run.
         const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-        const int want = std::max(1, std::min(64, (4 * cus + units - 1) / units));
+        const char *sp = getenv("RXQ4_ATTN_SPLIT");
+        const int cap = sp ? std::max(1, std::min(64, atoi(sp))) : 64;
+        const int want = std::max(1, std::min(cap, (4 * cus + units - 1) / units));
         int chunk = (seq0 + want - 1) / want;
         chunk = (chunk + kAttnTile - 1) / kAttnTile * kAttnTile;
         p.chunk = chunk;
