@@ -701,73 +701,127 @@ __device__ __forceinline__ void kq_fragments(__amdgpu_buffer_rsrc_t rs, int boff
     }
 }
 
-template <int T, int XT, int YT>
+template <int T, int XT, int YT, int RT, int TT>
 __global__ __launch_bounds__(256) void kq_tokens_kernel(void *__restrict__ y,
                                                         const uint8_t *__restrict__ w,
                                                         const uint16_t *__restrict__ x, int M,
                                                         int N, int K) {
     constexpr int BYTES = KqFormat<T>::kBytes;
-    __shared__ f32x4 part[4][64];
+    constexpr int NF = RT * TT;  // 16 x 16 output fragments per wave
+    __shared__ f32x4 part[4][NF][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int li = lane & 15, g = lane >> 4;
     const int nb = K >> 8;
     const int row_bytes = nb * BYTES;
-    const int row0 = blockIdx.x * 16;
-    const int tok0 = blockIdx.y * 16;
-    const int n_rows = min(16, M - row0), n_tok = min(16, N - tok0);
+    const int row0 = blockIdx.x * 16 * RT;
+    const int tok0 = blockIdx.y * 16 * TT;
+    const int n_rows = min(16 * RT, M - row0), n_tok = min(16 * TT, N - tok0);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(w + (int64_t)row0 * row_bytes, n_rows * row_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + (int64_t)tok0 * K, n_tok * K * 2);
-    const int xoff = li * K * 2 + 16 * g;
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[RT][TT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // K blocks round-robin over the 4 waves; each block's RT weight
+    // fragments are dequantised once and used for all TT token fragments.
     for (int b = wave; b < nb; b += 4) {
-        u32x4 a[8], bx[8];
+        u32x4 a[RT][8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) bx[t] = buffer_load16(xr, xoff + 2 * (256 * b + 32 * t));
-        kq_fragments<T, XT>(rs, li * row_bytes + b * BYTES, g, a);
+        for (int r = 0; r < RT; ++r)
+            kq_fragments<T, XT>(rs, (16 * r + li) * row_bytes + b * BYTES, g, a[r]);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) acc = mfma<XT>(a[t], bx[t], acc);
+        for (int t = 0; t < TT; ++t) {
+            u32x4 bx[8];
+            const int xoff = (16 * t + li) * K * 2 + 16 * g + 2 * 256 * b;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) bx[k] = buffer_load16(xr, xoff + 2 * 32 * k);
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[r][t] = mfma<XT>(a[r][k], bx[k], acc[r][t]);
+        }
     }
-    part[wave][lane] = acc;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) part[wave][r * TT + t][lane] = acc[r][t];
     __syncthreads();
-    if (wave == 0) {
-        f32x4 s = part[0][lane];
+    // Fragment f is reduced (waves in order) and stored by wave f % 4.
+    for (int f = wave; f < NF; f += 4) {
+        const int r = f / TT, t = f % TT;
+        f32x4 s = part[0][f][lane];
 #pragma unroll
         for (int j = 1; j < 4; ++j) {
-            const f32x4 o = part[j][lane];
+            const f32x4 o = part[j][f][lane];
             s = f32x4{s[0] + o[0], s[1] + o[1], s[2] + o[2], s[3] + o[3]};
         }
-        if (li < n_tok) {
+        const int tok = 16 * t + li;
+        if (tok < n_tok) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 4 * g + r;
-                if (row < n_rows) store_out<YT>(y, (int64_t)(tok0 + li) * M + row0 + row, s[r]);
+            for (int q = 0; q < 4; ++q) {
+                const int row = 16 * r + 4 * g + q;
+                if (row < n_rows) store_out<YT>(y, (int64_t)(tok0 + tok) * M + row0 + row, s[q]);
             }
         }
     }
+}
+
+template <int T, int XT, int YT, int RT, int TT>
+static void launch_kq_tok(dim3 grid, void *y, const uint8_t *w, const uint16_t *x, int M, int N,
+                          int K, hipStream_t st) {
+    kq_tokens_kernel<T, XT, YT, RT, TT><<<grid, 256, 0, st>>>(y, w, x, M, N, K);
+}
+
+// Tile: 32 rows when there are enough tiles to fill the chip, 16 x TT tokens
+// with TT up to 8 (one 16-token fragment for small batches).
+template <int T, int XT, int YT>
+static hipError_t launch_kq_tokens_xy(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
+                                      int K, hipStream_t st) {
+    const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+    // The largest tile (most reuse of each dequantised weight and x
+    // fragment) that still gives a workgroup per CU; tiles never exceed
+    // the token count (one workgroup per CU measured best at m = 512).
+    int tt = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8, rt = 2;
+    auto wgs = [&](int r, int t) {
+        return (int64_t)((M + 16 * r - 1) / (16 * r)) * ((N + 16 * t - 1) / (16 * t));
+    };
+    while (wgs(rt, tt) < cus && (rt > 1 || tt > 1)) {
+        if (rt > 1) rt = 1;
+        else tt /= 2;
+    }
+    const dim3 grid((M + 16 * rt - 1) / (16 * rt), (N + 16 * tt - 1) / (16 * tt));
+    if (grid.y > 65535) return hipErrorInvalidValue;
+    if (rt == 2) {
+        if (tt == 1) launch_kq_tok<T, XT, YT, 2, 1>(grid, y, w, x, M, N, K, st);
+        else if (tt == 2) launch_kq_tok<T, XT, YT, 2, 2>(grid, y, w, x, M, N, K, st);
+        else if (tt == 4) launch_kq_tok<T, XT, YT, 2, 4>(grid, y, w, x, M, N, K, st);
+        else launch_kq_tok<T, XT, YT, 2, 8>(grid, y, w, x, M, N, K, st);
+    } else {
+        if (tt == 1) launch_kq_tok<T, XT, YT, 1, 1>(grid, y, w, x, M, N, K, st);
+        else if (tt == 2) launch_kq_tok<T, XT, YT, 1, 2>(grid, y, w, x, M, N, K, st);
+        else if (tt == 4) launch_kq_tok<T, XT, YT, 1, 4>(grid, y, w, x, M, N, K, st);
+        else launch_kq_tok<T, XT, YT, 1, 8>(grid, y, w, x, M, N, K, st);
+    }
+    return hipGetLastError();
 }
 
 template <int T>
 static hipError_t launch_kq_tokens_t(void *y, int y_dtype, const uint8_t *w, const void *x,
                                      int x_dtype, int M, int N, int K, hipStream_t st) {
     const int64_t row_bytes = (int64_t)(K / 256) * KqFormat<T>::kBytes;
-    if (row_bytes * 16 > 0x7FFFFFFF || (int64_t)16 * K * 2 > 0x7FFFFFFF) return hipErrorInvalidValue;
-    const dim3 grid((M + 15) / 16, (N + 15) / 16);
-    if (grid.y > 65535) return hipErrorInvalidValue;
+    if (row_bytes * 32 > 0x7FFFFFFF || (int64_t)128 * K * 2 > 0x7FFFFFFF) return hipErrorInvalidValue;
     const uint16_t *xx = static_cast<const uint16_t *>(x);
     if (x_dtype == RXQ4_DTYPE_BF16) {
         if (y_dtype == RXQ4_DTYPE_BF16)
-            kq_tokens_kernel<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16><<<grid, 256, 0, st>>>(y, w, xx, M, N, K);
-        else
-            kq_tokens_kernel<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32><<<grid, 256, 0, st>>>(y, w, xx, M, N, K);
-    } else {
-        if (y_dtype == RXQ4_DTYPE_F16)
-            kq_tokens_kernel<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F16><<<grid, 256, 0, st>>>(y, w, xx, M, N, K);
-        else
-            kq_tokens_kernel<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F32><<<grid, 256, 0, st>>>(y, w, xx, M, N, K);
+            return launch_kq_tokens_xy<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, N, K, st);
+        return launch_kq_tokens_xy<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
     }
-    return hipGetLastError();
+    if (y_dtype == RXQ4_DTYPE_F16)
+        return launch_kq_tokens_xy<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, N, K, st);
+    return launch_kq_tokens_xy<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
 }
 
 hipError_t launch_kq_tokens(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,

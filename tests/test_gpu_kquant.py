@@ -147,7 +147,9 @@ def test_q6k_embedding_bit_exact(K):
 
 
 @pytest.mark.parametrize("t", [13, 14])
-@pytest.mark.parametrize("M,N,K", [(300, 2, 2048), (129, 17, 512), (64, 40, 11008), (33, 5, 256)])
+# token tiles of 16, 32, 64 and 128 (N 5..130), row tiles of 16 and 32
+@pytest.mark.parametrize("M,N,K", [(300, 2, 2048), (129, 17, 512), (64, 40, 11008), (33, 5, 256),
+                                   (600, 130, 1024), (2100, 70, 512)])
 def test_kq_gemm(t, M, N, K):
     print(f"kq gemm type {t} M={M} N={N} K={K}", flush=True)
     Wn = kb.random_blocks(t, util.rng(740 + t + N), M, K)
