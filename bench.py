@@ -21,10 +21,12 @@ stream and timed with HIP events recorded on that stream around replays:
   per_kernel   every decode projection, the LM head [151936 x 2048] fp32
                GEMV, the 4096-id Zipf(1.1) embedding gather, and the prefill
                GEMM at m=512 (TFLOP/s, BASELINE metric's second half)
-  attn_*       decode attention over 4096 positions and causal prefill of 512
-               tokens (32 query / 8 KV heads, head_dim 128, fp16 KV)
-  q6k_*        Q6_K (ggml type 14) LM head, embedding gather, down, and the
-               mixed Q4_K/Q4_K/Q6_K QKV triple (the Q4_K_M file layout)
+  attn_*       decode attention over 4096 and 16384 positions and causal
+               prefill of 512 tokens (32 query / 8 KV heads, head_dim 128,
+               fp16 KV)
+  q6k_*, q5k_* Q6_K (ggml type 14) LM head, embedding gather, down, the
+               mixed Q4_K/Q4_K/Q6_K QKV triple (the Q4_K_M file layout), and
+               the Q6_K / Q5_K prefill GEMM at m=512
   small_batch_decode  m in {1,2,4,8,16} tokens on gate+up and down
                (where weight reuse ends the purely
                bandwidth-bound regime)
@@ -408,6 +410,16 @@ def main() -> int:
         fl = 4.0 * AH * AD * sum(t + 1 for t in range(512))
         kernels["attn_prefill_fp16_512"] = {"us": round(med, 3), "TFLOPs": round(fl / med / 1e6, 2)}
         del caches
+        long_kv = [(gen(74_000 + i, (16384, AKV, AD), 1.0).half(), gen(75_000 + i, (16384, AKV, AD), 1.0).half())
+                   for i in range(2)]
+
+        def attn_long(i):
+            k, v = long_kv[i % 2]
+            capi.attention_decode_f16(oa, qa, k, v, AH, AKV, AD, 16384, AD ** -0.5, stream=sp)
+        med, _ = per_launch(attn_long, 20)
+        b = 2 * 16384 * AKV * AD * 2
+        kernels["attn_decode_fp16_16384"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
+        del long_kv
 
         # Small-batch decode: m tokens through
         # gemm_quant_batched's C-ABI form with fp16 x / y on the decode
@@ -441,6 +453,20 @@ def main() -> int:
             del ws
         extras["gemm_m512_tflops"] = min(v["TFLOPs"] for k, v in kernels.items()
                                          if k.startswith("gemm_bf16_m512"))
+        # The same prefill GEMM on Q6_K and Q5_K weights (Q4_K_M files keep
+        # some FFN and V tensors in these formats).
+        for t, tname in ((14, "q6k"), (13, "q5k")):
+            for (M, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):
+                ws = [qweights(31_000 + M + i, M, K, ggml_type=t) for i in range(2)]
+                xb = gen(41_000 + K, (512, K), 1.0).to(torch.bfloat16)
+                yb = torch.empty((512, M), dtype=torch.bfloat16, device=dev)
+
+                def kq_launch(i, ws=ws, xb=xb, yb=yb, M=M, K=K, t=t):
+                    capi.gemm(yb, ws[i % 2], xb, M, 512, K, stream=sp, ggml_type=t)
+                med, _ = per_launch(kq_launch, 6)
+                tf = 2 * 512 * M * K / med / 1e6
+                kernels[f"{tname}_gemm_bf16_m512_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1)}
+                del ws
 
     # ------------------------------------------------------- CPU baseline
     cpu = None
