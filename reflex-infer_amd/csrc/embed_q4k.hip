@@ -1,71 +1,74 @@
 // embed_q4k.hip -- Q4_K embedding-row dequantisation for gfx950.
 //
 // Replaces dequant_embedding_q4k_kernel (reference q4_gemm.cu:545-572) and
-// adds the batched gather the reference API cannot express.  A thread owns 8
-// consecutive outputs of one row: it reads the 16-byte block header and 8
-// quant bytes, computes w = (d*sc)*q - dmin*m in fp32 (one rounding, as the
-// reference) and writes 8 fp16 (RNE) values with one 16-byte store.  Only the
-// addressed rows are read.  Bytes per launch: unique_rows*K/256*144 (header
+// adds the batched gather the reference API cannot express.  A thread owns
+// 16 consecutive outputs of one row: it reads the 16-byte block header and
+// 16 quant bytes, computes w = (d*sc)*q - dmin*m in fp32 (one rounding, as
+// the reference) and writes 16 fp16 (RNE) values with two 16-byte stores.
+// Only the addressed rows are read.  Bytes per launch: unique_rows*K/256*144 (header
 // reads are L2 hits after the first) + n_ids*K*2 written + n_ids*4 ids.
 #include "launch.h"
 #include "q4k_device.h"
 
 namespace rxq4 {
 
+// A thread owns 16 consecutive outputs (half a sub-block) of one row: the
+// 16-byte header, 16 quant bytes (one load, nibble half of the sub-block)
+// and two 16-byte stores.
 template <bool kBatched>
 __global__ __launch_bounds__(256) void embed_kernel(uint16_t *__restrict__ dst,
                                                     const uint8_t *__restrict__ w,
                                                     const int32_t *__restrict__ ids,
                                                     int token_id, int64_t n_vocab,
                                                     int n_ids, int K) {
-    const int per_row = K >> 3;
+    const int per_row = K >> 4;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t i = t / per_row;
     const int c = (int)(t - i * per_row);
     if (i >= n_ids) return;
-    u32x4 *out = reinterpret_cast<u32x4 *>(dst + i * K + c * 8);
+    u32x4 *out = reinterpret_cast<u32x4 *>(dst + i * K + c * 16);
     int64_t id = token_id;
     if (kBatched) {
         id = ids[i];
         if (id < 0 || id >= n_vocab) {
-            *out = u32x4{0, 0, 0, 0};
+            out[0] = u32x4{0, 0, 0, 0};
+            out[1] = u32x4{0, 0, 0, 0};
             return;
         }
     }
     const int nb = K >> 8;
-    const int e0 = c * 8;
-    const int b = e0 >> 8;
-    const int pos = e0 & 255;
-    const int il = pos >> 6;
-    const int hi = (pos >> 5) & 1;
-    const int l0 = pos & 31;
+    const int e0 = c * 16;
+    const int b = e0 >> 8, pos = e0 & 255;
+    const int il = pos >> 6, hi = (pos >> 5) & 1, l0 = pos & 31;
     const uint8_t *blk = w + (id * nb + b) * kBlockBytes;
     const u32x4 h = load16(blk);
-    const u32x2 q = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * il + l0);
+    const u32x4 q = load16(blk + 16 + 32 * il + l0);
     const float d = f16_bits_to_f32(h.x & 0xFFFFu);
     const float dmin = f16_bits_to_f32(h.x >> 16);
     uint32_t sc, mn;
     scale_one(h.y, h.z, h.w, 2 * il + hi, &sc, &mn);
     const float ds = d * (float)sc;
     const float dm = dmin * (float)mn;
-    uint32_t packed[4];
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    uint32_t packed[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t word = j < 2 ? q.x : q.y;
-        const int sh0 = (2 * j & 3) * 8, sh1 = sh0 + 8;
-        uint32_t b0 = (word >> sh0) & 0xFFu, b1 = (word >> sh1) & 0xFFu;
+    for (int k = 0; k < 8; ++k) {  // outputs 2k, 2k + 1 = bytes 2k, 2k + 1
+        const uint32_t word = qw[k >> 1];
+        const int sh = (k & 1) * 16;
+        uint32_t b0 = (word >> sh) & 0xFFu, b1 = (word >> (sh + 8)) & 0xFFu;
         b0 = hi ? (b0 >> 4) : (b0 & 0xFu);
         b1 = hi ? (b1 >> 4) : (b1 & 0xFu);
         const float v0 = ds * (float)b0 - dm;
         const float v1 = ds * (float)b1 - dm;
-        packed[j] = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
+        packed[k] = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
     }
-    *out = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    out[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    out[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
 }
 
 hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
                         int64_t n_vocab, int n_ids, int K, hipStream_t st) {
-    const int64_t threads = (int64_t)n_ids * (K >> 3);
+    const int64_t threads = (int64_t)n_ids * (K >> 4);
     const int64_t grid = (threads + 255) / 256;
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;

@@ -566,17 +566,18 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ d
                                                         int token_id, int64_t n_vocab, int n_ids,
                                                         int K) {
     constexpr int BYTES = KqFormat<14>::kBytes;
-    const int per_row = K >> 3;
+    const int per_row = K >> 4;  // 16-value sub-blocks (one int8 scale each)
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t i = t / per_row;
     const int c = (int)(t - i * per_row);
     if (i >= n_ids) return;
-    u32x4 *out = reinterpret_cast<u32x4 *>(dst + i * K + c * 8);
+    u32x4 *out = reinterpret_cast<u32x4 *>(dst + i * K + c * 16);
     int64_t id = token_id;
     if (kBatched) {
         id = ids[i];
         if (id < 0 || id >= n_vocab) {
-            *out = u32x4{0, 0, 0, 0};
+            out[0] = u32x4{0, 0, 0, 0};
+            out[1] = u32x4{0, 0, 0, 0};
             return;
         }
     }
@@ -584,7 +585,7 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ d
     const int row_bytes = nb * BYTES;
     const RowRes rr = row_rsrc(w + id * row_bytes, row_bytes);
     const __amdgpu_buffer_rsrc_t rs = rr.rs;
-    const int e0 = c * 8;
+    const int e0 = c * 16;
     const int boff = rr.ex + (e0 >> 8) * BYTES;
     const int pos = e0 & 255;
     const int h = pos >> 7, j = (pos >> 5) & 3, l0 = pos & 31;
@@ -596,9 +597,9 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ d
     // scale 8h + 2j + l0/16: dword 2h + (j >> 1), byte 2(j & 1) + l0/16
     const uint32_t sw = h ? ((j & 2) ? S.w : S.z) : ((j & 2) ? S.y : S.x);
     const float ds = d * scale_byte(sw, 2 * (j & 1) + (l0 >> 4));
-    uint32_t packed[4];
+    uint32_t packed[8];
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
+    for (int m = 0; m < 4; ++m) {
         // ql word m holds weights 4m..4m+3 of this thread in nibble j>>1,
         // qh word m their high bits at 2j.
         const uint32_t lo = ((j & 2) ? (ql[m] >> 4) : ql[m]) & 0x0F0F0F0Fu;
@@ -615,12 +616,13 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ d
             packed[2 * m + e] = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
         }
     }
-    *out = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    out[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    out[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
 }
 
 hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
                            int64_t n_vocab, int n_ids, int K, hipStream_t st) {
-    const int64_t threads = (int64_t)n_ids * (K / 8);
+    const int64_t threads = (int64_t)n_ids * (K / 16);
     const int64_t grid = (threads + 255) / 256;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (ids)
