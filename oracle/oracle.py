@@ -200,7 +200,9 @@ def gemv_f64(W, K, x32) -> np.ndarray:
 
 
 def gemm_f64(W, K, x32, wkind: str) -> np.ndarray:
-    """fp64 GEMM with weights rounded to 'f16' or 'bf16'; x32 [N, K] fp32 values."""
+    """fp64 GEMM with weights rounded to 'f16' or 'bf16'; x32 [N, K] fp32 values.
+    (Unrounded weights: kq_gemm_f64(W, K, 12, x32, None).)"""
+    assert wkind in ("f16", "bf16"), wkind
     W = _w(W, K)
     x32 = np.ascontiguousarray(x32, dtype=np.float32)
     N = x32.shape[0]

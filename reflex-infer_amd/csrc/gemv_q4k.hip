@@ -23,6 +23,7 @@
 // K*2 + rows*out_bytes (+ rows*2 residual).
 #include "launch.h"
 #include "q4k_device.h"
+#include "rxq4.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -130,6 +131,53 @@ __device__ __forceinline__ void group_dot(u32x4 q0, u32x4 q1, const XSlot &s, ui
     }
 }
 
+// group_dot for NT tokens: the nibble pairs are formed once and multiplied
+// into every token's accumulators.
+template <int NT>
+__device__ __forceinline__ void group_dot_nt(u32x4 q0, u32x4 q1, const XSlot *s, uint32_t magic,
+                                             float *acc_lo, float *acc_hi) {
+    const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t v = q[k], v8 = q[k] >> 8;
+        const uint32_t w0 = and_or(v, 0x000F000Fu, magic);
+        const uint32_t w1 = and_or(v8, 0x000F000Fu, magic);
+        const uint32_t w2 = and_or(v, 0x00F000F0u, magic);
+        const uint32_t w3 = and_or(v8, 0x00F000F0u, magic);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            acc_lo[t] = __builtin_amdgcn_fdot2(as_half2(w0), as_half2(s[t].p[4 * k + 0]), acc_lo[t], false);
+            acc_hi[t] = __builtin_amdgcn_fdot2(as_half2(w2), as_half2(s[t].p[4 * k + 2]), acc_hi[t], false);
+            acc_lo[t] = __builtin_amdgcn_fdot2(as_half2(w1), as_half2(s[t].p[4 * k + 1]), acc_lo[t], false);
+            acc_hi[t] = __builtin_amdgcn_fdot2(as_half2(w3), as_half2(s[t].p[4 * k + 3]), acc_hi[t], false);
+        }
+    }
+}
+
+// Partial dot products of one slot of one row with NT tokens' activations.
+template <int NT>
+__device__ __forceinline__ void slot_dot_nt(u32x4 hdr, u32x4 q0, u32x4 q1, const XSlot *s,
+                                            const ScaleDecode &sd, uint32_t magic, float *out) {
+    const float d = f16_bits_to_f32(hdr.x & 0xFFFFu);
+    const float dmin = f16_bits_to_f32(hdr.x >> 16);
+    const uint32_t sc = ((hdr.y >> sd.shA) & sd.mA) | ((hdr.w >> sd.shC) & sd.mC);
+    const uint32_t mn = ((hdr.z >> sd.shA) & sd.mA) | ((hdr.w >> sd.shC4) & sd.mC);
+    float acc_lo[NT], acc_hi[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        acc_lo[t] = s[t].bias_lo;
+        acc_hi[t] = s[t].bias_hi;
+    }
+    group_dot_nt<NT>(q0, q1, s, magic, acc_lo, acc_hi);
+    const float d_lo = d * (float)(sc & 0xFFu);
+    const float d_hi = (d * 0.0625f) * (float)((sc >> 8) & 0xFFu);
+    const float m_lo = dmin * (float)(mn & 0xFFu);
+    const float m_hi = dmin * (float)((mn >> 8) & 0xFFu);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        out[t] = d_lo * acc_lo[t] - m_lo * s[t].sx_lo + (d_hi * acc_hi[t] - m_hi * s[t].sx_hi);
+}
+
 // Partial dot product of one slot of one row.
 __device__ __forceinline__ float slot_dot(u32x4 hdr, u32x4 q0, u32x4 q1, const XSlot &s,
                                           const ScaleDecode &sd, uint32_t magic) {
@@ -204,13 +252,15 @@ __device__ __forceinline__ Range range_of_unit(const GemvParams &p, int unit) {
     return r;
 }
 
-// `res` is the fp16 residual of the row (kEpiAdd), loaded with the weights.
+// `res` is the fp16 residual of the row (kEpiAdd), loaded with the weights;
+// `yoff` the output offset of the token (multi-token calls).
 template <int EPI>
-__device__ __forceinline__ void store_row(const Range &r, int row, float v, uint32_t res) {
+__device__ __forceinline__ void store_row(const Range &r, int row, float v, uint32_t res,
+                                          int64_t yoff = 0) {
     if (EPI == kEpiF32) {
-        static_cast<float *>(r.y)[row] = v;
+        static_cast<float *>(r.y)[yoff + row] = v;
     } else if (EPI == kEpiF16) {
-        static_cast<uint16_t *>(r.y)[row] = f32_to_f16_bits(v);
+        static_cast<uint16_t *>(r.y)[yoff + row] = f32_to_f16_bits(v);
     } else {
         // q4_gemm.cu:774-777: round the projection, add the residual, round.
         const float projected = f16_bits_to_f32(f32_to_f16_bits(v));
@@ -249,11 +299,11 @@ struct Batch {
 constexpr int kRegMaxK = 4096;
 constexpr int kRegMaxRows = 256;
 
-template <int LPR, int EPI, int U>
+template <int LPR, int EPI, int U, int NT>
 __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
     constexpr int RPS = 64 / LPR;
-    __shared__ __attribute__((aligned(16))) uint16_t xsh[kRegMaxK];
-    __shared__ float outs[4][kRegMaxRows];
+    __shared__ __attribute__((aligned(16))) uint16_t xsh[NT][kRegMaxK];
+    __shared__ float outs[NT][4][kRegMaxRows];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -273,14 +323,18 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
     const uint32_t hdr_off = (uint32_t)b * kBlockBytes;
     const uint32_t q_off = hdr_off + 16u + 32u * (uint32_t)il;
 
-    // x -> LDS: chunk c (16 bytes) of thread c + 256*round; chunks past K
-    // read as zeros.
+    // x -> LDS: chunk c (16 bytes) of thread c + 256*round, per token;
+    // chunks past K read the next token's x or, past the last, zeros (the
+    // staged positions past K are never read).
     const int x_bytes = p.nb * kQK * 2;
-    const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(p.x, x_bytes);
+    const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(p.x, NT * x_bytes);
     constexpr int kXRounds = (RPS == 1) ? 2 : 1;  // K = 4096 only with LPR = 64
 #pragma unroll
-    for (int r = 0; r < kXRounds; ++r)
-        buffer_to_lds16(xrsrc, &xsh[(256 * r + 64 * wv) * 8], (256 * r + tid) * 16);
+    for (int tk = 0; tk < NT; ++tk)
+#pragma unroll
+        for (int r = 0; r < kXRounds; ++r)
+            buffer_to_lds16(xrsrc, &xsh[tk][(256 * r + 64 * wv) * 8],
+                            tk * x_bytes + (256 * r + tid) * 16);
     __builtin_amdgcn_sched_barrier(0);  // the counted loads below stay behind the copies
 
     // Weights.  Steps past t1 reload step t1-1 (inactive waves: step 0; L2
@@ -309,12 +363,15 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
     wait_vmcnt<kWeightLoads>();  // this wave's x copies have landed
     lds_barrier();               // ... and every other wave's
 
-    u32x4 xraw[8];
-    const u32x4 *xs16 = reinterpret_cast<const u32x4 *>(xsh) + b * 32 + il * 8;
+    XSlot xs[NT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xraw[i] = xs16[i];
-    XSlot xs;
-    x_slot_from_raw(xraw, xs);
+    for (int tk = 0; tk < NT; ++tk) {
+        u32x4 xraw[8];
+        const u32x4 *xs16 = reinterpret_cast<const u32x4 *>(xsh[tk]) + b * 32 + il * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xraw[i] = xs16[i];
+        x_slot_from_raw(xraw, xs[tk]);
+    }
     const ScaleDecode sd = scale_decode_for(il);
     const uint32_t magic = magic_vgpr();
     const int n = t1 - t0;
@@ -322,9 +379,16 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (t + u < n) {  // uniform
-                float v = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic);
-                v = lane_group_sum<LPR>(v);
-                if (slot == LPR - 1) outs[wv][(t + u) * RPS + sub] = v;
+                float v[NT];
+                if (NT == 1)
+                    v[0] = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs[0], sd, magic);
+                else
+                    slot_dot_nt<NT>(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic, v);
+#pragma unroll
+                for (int tk = 0; tk < NT; ++tk) {
+                    const float r = lane_group_sum<LPR>(v[tk]);
+                    if (slot == LPR - 1) outs[tk][wv][(t + u) * RPS + sub] = r;
+                }
             }
         }
     };
@@ -347,11 +411,16 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
     // Coalesced stores of the wave's rows (same-wave LDS traffic is in
     // order, so the results written above are visible here).
     const int rows = min(n * RPS, rg.rows - row0);
-    if (lane < rows) store_row<EPI>(rg, row0 + lane, outs[wv][lane], res);
-    for (int r = 64; r < rows; r += 64) {
-        const int row = row0 + r + lane;
-        if (r + lane < rows)
-            store_row<EPI>(rg, row, outs[wv][r + lane], EPI == kEpiAdd ? rg.res[row] : 0u);
+#pragma unroll
+    for (int tk = 0; tk < NT; ++tk) {
+        const int64_t yoff = (int64_t)tk * p.y_stride;
+        if (lane < rows) store_row<EPI>(rg, row0 + lane, outs[tk][wv][lane], res, yoff);
+        for (int r = 64; r < rows; r += 64) {
+            const int row = row0 + r + lane;
+            if (r + lane < rows)
+                store_row<EPI>(rg, row, outs[tk][wv][r + lane], EPI == kEpiAdd ? rg.res[row] : 0u,
+                               yoff);
+        }
     }
 }
 
@@ -367,7 +436,7 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 constexpr int kLdsSlotWords = 36;
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <int EPI, int U>
+template <int EPI, int U, int NT>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
     extern __shared__ uint32_t xlds[];
     const int lane = threadIdx.x & 63;
@@ -401,8 +470,10 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
             if (++ld_j == J) { ld_j = 0; ++ld_row; }
         }
     };
-    // Stage x, one slot per thread and round; the first round's loads go out
-    // before the weights (vector loads complete in order).
+    // Stage x, one slot per thread and round (token tk's slots follow token
+    // tk - 1's); the first round's loads go out before the weights (vector
+    // loads complete in order).
+    const int K = 256 * p.nb;
     auto stage = [&](int s, const u32x4 raw[8]) {
         XSlot xs;
         x_slot_from_raw(raw, xs);
@@ -415,23 +486,32 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
     };
     const int s_first = threadIdx.x;
     const int s_load = min(s_first, n_slots - 1);
-    u32x4 xraw[8];
-    load_x_raw(p.x, s_load >> 2, s_load & 3, xraw);
+    u32x4 xraw[NT][8];
+#pragma unroll
+    for (int tk = 0; tk < NT; ++tk) load_x_raw(p.x + (int64_t)tk * K, s_load >> 2, s_load & 3, xraw[tk]);
     __builtin_amdgcn_sched_barrier(0);
     Batch<U> A, B;
     load(A);
     load(B);
     __builtin_amdgcn_sched_barrier(0);
-    if (s_first < n_slots) stage(s_first, xraw);
+    if (s_first < n_slots) {
+#pragma unroll
+        for (int tk = 0; tk < NT; ++tk) stage(tk * n_slots + s_first, xraw[tk]);
+    }
     for (int s = s_first + blockDim.x; s < n_slots; s += blockDim.x) {
-        load_x_raw(p.x, s >> 2, s & 3, xraw);
-        stage(s, xraw);
+#pragma unroll
+        for (int tk = 0; tk < NT; ++tk) {
+            load_x_raw(p.x + (int64_t)tk * K, s >> 2, s & 3, xraw[0]);
+            stage(tk * n_slots + s, xraw[0]);
+        }
     }
     __syncthreads();
     if (n_items == 0) return;
 
     const uint32_t magic = magic_vgpr();
-    float acc = 0.0f;
+    float acc[NT];
+#pragma unroll
+    for (int tk = 0; tk < NT; ++tk) acc[tk] = 0.0f;
     int cp_item = 0, cp_row = r0, cp_j = 0;
     auto compute = [&](const Batch<U> &bt) {
 #pragma unroll
@@ -440,26 +520,39 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
                 const int slot = 64 * cp_j + lane;
                 const bool valid = slot < n_slots;
                 const int sl = valid ? slot : 0;
-                const uint32_t *src = xlds + sl * kLdsSlotWords;
-                XSlot xs;
+                XSlot xs[NT];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(src + 4 * k);
-                    xs.p[4 * k] = v.x; xs.p[4 * k + 1] = v.y; xs.p[4 * k + 2] = v.z; xs.p[4 * k + 3] = v.w;
+                for (int tk = 0; tk < NT; ++tk) {
+                    const uint32_t *src = xlds + (tk * n_slots + sl) * kLdsSlotWords;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const u32x4 v = *reinterpret_cast<const u32x4 *>(src + 4 * k);
+                        xs[tk].p[4 * k] = v.x; xs[tk].p[4 * k + 1] = v.y;
+                        xs[tk].p[4 * k + 2] = v.z; xs[tk].p[4 * k + 3] = v.w;
+                    }
+                    const f32x4v t = *reinterpret_cast<const f32x4v *>(src + 32);
+                    xs[tk].bias_lo = t[0];
+                    xs[tk].bias_hi = t[1];
+                    xs[tk].sx_lo = t[2];
+                    xs[tk].sx_hi = t[3];
                 }
-                const f32x4v t = *reinterpret_cast<const f32x4v *>(src + 32);
-                xs.bias_lo = t[0];
-                xs.bias_hi = t[1];
-                xs.sx_lo = t[2];
-                xs.sx_hi = t[3];
                 const ScaleDecode sd = scale_decode_for(sl & 3);
-                const float v = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic);
-                acc += valid ? v : 0.0f;
+                float v[NT];
+                if (NT == 1)
+                    v[0] = slot_dot(bt.h[u], bt.a[u], bt.c[u], xs[0], sd, magic);
+                else
+                    slot_dot_nt<NT>(bt.h[u], bt.a[u], bt.c[u], xs, sd, magic, v);
+#pragma unroll
+                for (int tk = 0; tk < NT; ++tk) acc[tk] += valid ? v[tk] : 0.0f;
                 ++cp_item;
                 if (++cp_j == J) {
-                    const float total = lane_group_sum<64>(acc);
-                    if (lane == 63) store_row<EPI>(rg, cp_row, total, bt.r[u]);
-                    acc = 0.0f;
+#pragma unroll
+                    for (int tk = 0; tk < NT; ++tk) {
+                        const float total = lane_group_sum<64>(acc[tk]);
+                        if (lane == 63)
+                            store_row<EPI>(rg, cp_row, total, bt.r[u], (int64_t)tk * p.y_stride);
+                        acc[tk] = 0.0f;
+                    }
                     cp_j = 0;
                     ++cp_row;
                 }
@@ -527,12 +620,12 @@ static int assign_units(GemvParams &p, int rows_per_item, int per_unit) {
 #endif
 constexpr int kRegBatch = RXQ4_GEMV_BATCH;
 
-template <int LPR, int EPI>
+template <int LPR, int EPI, int NT>
 static void launch_reg(const GemvParams &p, int grid, hipStream_t st) {
-    gemv_reg_kernel<LPR, EPI, kRegBatch><<<grid, 256, 0, st>>>(p);
+    gemv_reg_kernel<LPR, EPI, kRegBatch, NT><<<grid, 256, 0, st>>>(p);
 }
 
-template <int EPI>
+template <int EPI, int NT>
 static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
     const int slots = 4 * p.nb;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
@@ -546,15 +639,15 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         const int waves = assign_units(p, rps, per_wave);
         const int grid = (waves + 3) / 4;
         switch (slots) {
-            case 4: launch_reg<4, EPI>(p, grid, st); break;
-            case 8: launch_reg<8, EPI>(p, grid, st); break;
-            case 16: launch_reg<16, EPI>(p, grid, st); break;
-            case 32: launch_reg<32, EPI>(p, grid, st); break;
-            default: launch_reg<64, EPI>(p, grid, st); break;
+            case 4: launch_reg<4, EPI, NT>(p, grid, st); break;
+            case 8: launch_reg<8, EPI, NT>(p, grid, st); break;
+            case 16: launch_reg<16, EPI, NT>(p, grid, st); break;
+            case 32: launch_reg<32, EPI, NT>(p, grid, st); break;
+            default: launch_reg<64, EPI, NT>(p, grid, st); break;
         }
     } else {
         // LDS kernel: whole rows per wave, `waves_per_cu` waves per CU.
-        const size_t lds = (size_t)slots * kLdsSlotWords * sizeof(uint32_t);
+        const size_t lds = (size_t)NT * slots * kLdsSlotWords * sizeof(uint32_t);
         if (lds > 160 * 1024) return hipErrorInvalidValue;
         const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_LDS_WAVES_PER_CU", 4);
         int per_wave = (int)((p.total_rows + target - 1) / target);
@@ -563,22 +656,48 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         const int grid = (waves + 3) / 4;
         if (lds > 64 * 1024) {
             const hipError_t e = hipFuncSetAttribute(
-                reinterpret_cast<const void *>(&gemv_lds_kernel<EPI, 2>),
+                reinterpret_cast<const void *>(&gemv_lds_kernel<EPI, 2, NT>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
-        gemv_lds_kernel<EPI, 2><<<grid, 256, lds, st>>>(p);
+        gemv_lds_kernel<EPI, 2, NT><<<grid, 256, lds, st>>>(p);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_gemv(GemvParams p, int epilogue, hipStream_t st) {
+    p.n_tok = 1;
+    p.y_stride = 0;
     switch (epilogue) {
-        case kEpiF16: return launch_gemv_epi<kEpiF16>(p, st);
-        case kEpiF32: return launch_gemv_epi<kEpiF32>(p, st);
-        case kEpiAdd: return launch_gemv_epi<kEpiAdd>(p, st);
+        case kEpiF16: return launch_gemv_epi<kEpiF16, 1>(p, st);
+        case kEpiF32: return launch_gemv_epi<kEpiF32, 1>(p, st);
+        case kEpiAdd: return launch_gemv_epi<kEpiAdd, 1>(p, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+template <int EPI>
+static hipError_t launch_multi_epi(GemvParams &p, int n_tok, hipStream_t st) {
+    switch (n_tok) {
+        case 2: return launch_gemv_epi<EPI, 2>(p, st);
+        case 3: return launch_gemv_epi<EPI, 3>(p, st);
+        default: return launch_gemv_epi<EPI, 4>(p, st);
+    }
+}
+
+hipError_t launch_gemv_multi_token(void *y, int y_dtype, const uint8_t *w, const uint16_t *x,
+                                   int M, int n_tok, int K, hipStream_t st) {
+    if (n_tok < 2 || n_tok > kMaxRegTokens) return hipErrorInvalidValue;
+    GemvParams p{};
+    p.r[0] = GemvRange{w, y, nullptr, M};
+    p.n_ranges = 1;
+    p.total_rows = M;
+    p.x = x;
+    p.nb = K / 256;
+    p.n_tok = n_tok;
+    p.y_stride = M;
+    return y_dtype == RXQ4_DTYPE_F32 ? launch_multi_epi<kEpiF32>(p, n_tok, st)
+                                     : launch_multi_epi<kEpiF16>(p, n_tok, st);
 }
 
 }  // namespace rxq4

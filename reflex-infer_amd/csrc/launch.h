@@ -30,7 +30,17 @@ struct GemvParams {
     int per_unit;        // steps per wave (register kernel) / rows per workgroup (split)
     int unit_start[3];   // first unit of ranges 1..2 in [1], [2]; [0] = 0
     int total_units;
+    int n_tok;           // tokens (1..kMaxRegTokens): x[t*K], y[t*y_stride + row]; one range if > 1
+    int y_stride;
 };
+
+// Token counts the decode GEMV kernels take in one pass (one weight read).
+constexpr int kMaxRegTokens = 4;
+
+// Multi-token decode GEMV, 2 <= n_tok <= kMaxRegTokens, fp16 x [n_tok x K],
+// y fp16 or fp32 [n_tok x M] (token-major).
+hipError_t launch_gemv_multi_token(void *y, int y_dtype, const uint8_t *w, const uint16_t *x,
+                                   int M, int n_tok, int K, hipStream_t stream);
 
 struct DeviceInfo {
     int cu_count;

@@ -7,6 +7,7 @@
 #include "rxq4.h"
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -168,6 +169,13 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
     return from_hip(rxq4::launch_gemv(p, rxq4::kEpiF16, st), fn);
 }
 
+// RXQ4_MULTI_TOKEN_GEMV=0 sends 2..4-token products to the MFMA small-batch
+// kernel instead (for comparisons).
+static bool multi_token_gemv() {
+    const char *v = getenv("RXQ4_MULTI_TOKEN_GEMV");
+    return !(v && v[0] == '0');
+}
+
 int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x, int x_dtype,
               int M, int N, int K, void *stream) {
     const char *fn = "rxq4_gemm";
@@ -195,6 +203,11 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
     if (kquant_type(ggml_type))
         e = rxq4::launch_kq_tokens(ggml_type, y, y_dtype, static_cast<const uint8_t *>(w), x,
                                    x_dtype, M, N, K, st);
+    else if (N <= rxq4::kMaxRegTokens && x_dtype == RXQ4_DTYPE_F16 && multi_token_gemv())
+        // 2..4 fp16 tokens: the decode GEMV with every token's activations in
+        // registers (one weight read, the nibble decode shared by the tokens)
+        e = rxq4::launch_gemv_multi_token(y, y_dtype, static_cast<const uint8_t *>(w),
+                                          static_cast<const uint16_t *>(x), M, N, K, st);
     else if (N <= rxq4::kMaxSmallBatch)
         e = rxq4::launch_gemv_tokens(y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M,
                                      N, K, st);

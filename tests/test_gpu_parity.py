@@ -298,7 +298,10 @@ def test_api_gemm_quant_batched_f16(M, N, K):
     Wn = util.weights(110 + N, M, K)
     x16 = util.x_f16(111 + N, (N, K))
     ref32 = orc.gemm_tokens_f32(Wn, K, x16)   # reference CPU semantics (per-token GEMV)
-    ref64 = orc.gemm_f64(Wn, K, f16(x16), "f16")  # same operands as the fp16 MFMA tiles
+    # the same operands as the kernel: up to 4 tokens run the decode GEMV on
+    # the exact weights, more tokens the MFMA tiles on fp16-rounded weights
+    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if N <= 4
+             else orc.gemm_f64(Wn, K, f16(x16), "f16"))
     W, x = dev(Wn), dev(x16)
     y = torch.empty((N, M), dtype=torch.float16, device="cuda")
     a = api.GemmQuantBatchedArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=12,
@@ -307,6 +310,31 @@ def test_api_gemm_quant_batched_f16(M, N, K):
     got = f16(host16(y))
     assert util.rel_err(got, ref32) <= util.TOL
     assert util.rounded_ok(host16(y), ref64).all()
+
+
+# 2..4 fp16 tokens: the decode GEMV kernels with every token's activations in
+# registers (register kernel for K 256..4096, LDS kernel for 1536 / 11008).
+@pytest.mark.parametrize("M,N,K", [(300, 2, 2048), (2048, 4, 2048), (129, 3, 11008),
+                                   (70, 4, 1536), (33, 2, 256), (17, 4, 4096), (5000, 2, 512)])
+def test_multi_token_gemv_equals_per_token_gemv(M, N, K):
+    print(f"multi-token GEMV M={M} N={N} K={K}", flush=True)
+    Wn = util.weights(140 + N + K, M, K)
+    x16 = util.x_f16(141 + N, (N, K))
+    ref32 = orc.gemm_tokens_f32(Wn, K, x16)
+    W, x = dev(Wn), dev(x16)
+    y16 = torch.empty((N, M), dtype=torch.float16, device="cuda")
+    capi.gemm_f16(y16, W, x, M, N, K)
+    y32 = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    capi.gemm(y32, W, x.view(torch.float16), M, N, K)
+    assert util.rel_err(y32.cpu().numpy(), ref32) <= util.TOL
+    assert util.rounded_ok(host16(y16), ref32).all()
+    # the same arithmetic, in the same order, as one GEMV per token
+    for t in range(N):
+        g16 = torch.empty(M, dtype=torch.float16, device="cuda")
+        g32 = torch.empty(M, dtype=torch.float32, device="cuda")
+        capi.gemv_f16(g16, W, x[t], M, K)
+        capi.gemv_f32(g32, W, x[t], M, K)
+        assert torch.equal(y16[t], g16) and torch.equal(y32[t], g32)
 
 
 def test_gemm_n1_is_the_gemv():
