@@ -484,33 +484,50 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(AttnParams p, int start
             qf[ks] = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks + 8 * g);
     }
 
-    // Staging registers: K chunks row-major (16 lanes per row: coalesced),
-    // V chunks position-major (consecutive lanes, consecutive positions: the
-    // transposed LDS writes do not collide).
-    u32x4 kr[NST], vr[NST];
-    float ksr = 1.0f, vsr = 1.0f;
-    auto load_tile = [&](int p0) {
+    // Staging registers, a ring of two tiles (tile j in set j & 1, loaded
+    // two iterations before it is used): K chunks row-major (16 lanes per
+    // row: coalesced); V in units of 4 consecutive positions x 8 dims, so
+    // the transposed LDS writes are 8 bytes (4 positions of one dim).
+    constexpr int NVU = kAttnTile / 4 * KCH;          // V units per tile
+    constexpr int NSV = (NVU + 255) / 256;            // V units per thread
+    struct Stage {
+        u32x4 k[NST];
+        u32x4 v[NSV][4];
+        float ks, vs;
+    };
+    auto load_tile = [&](int p0, Stage &S) {
 #pragma unroll
         for (int j = 0; j < NST; ++j) {
             const int id = tid + 256 * j;
             const int kpos = min(p0 + id / KCH, pos_end - 1), kc = id % KCH;
-            const int vpos = min(p0 + id % kAttnTile, pos_end - 1), vc = id / kAttnTile;
             const uint8_t *krow = kb + kpos * row_stride;
-            const uint8_t *vrow = vb + vpos * row_stride;
             if (I8) {
                 const u32x2 a = reinterpret_cast<const u32x2 *>(krow)[kc];
-                const u32x2 b = reinterpret_cast<const u32x2 *>(vrow)[vc];
-                kr[j] = u32x4{a.x, a.y, 0u, 0u};
-                vr[j] = u32x4{b.x, b.y, 0u, 0u};
+                S.k[j] = u32x4{a.x, a.y, 0u, 0u};
             } else {
-                kr[j] = reinterpret_cast<const u32x4 *>(krow)[kc];
-                vr[j] = reinterpret_cast<const u32x4 *>(vrow)[vc];
+                S.k[j] = reinterpret_cast<const u32x4 *>(krow)[kc];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NSV; ++j) {
+            const int id = min(tid + 256 * j, NVU - 1);  // threads past the units reload the last
+            const int q4 = id % (kAttnTile / 4), vc = id / (kAttnTile / 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int vpos = min(p0 + 4 * q4 + e, pos_end - 1);
+                const uint8_t *vrow = vb + vpos * row_stride;
+                if (I8) {
+                    const u32x2 b = reinterpret_cast<const u32x2 *>(vrow)[vc];
+                    S.v[j][e] = u32x4{b.x, b.y, 0u, 0u};
+                } else {
+                    S.v[j][e] = reinterpret_cast<const u32x4 *>(vrow)[vc];
+                }
             }
         }
         if (I8 && tid < kAttnTile) {
             const int pos = min(p0 + tid, pos_end - 1);
-            ksr = ksp[(int64_t)pos * s_stride];
-            vsr = vsp[(int64_t)pos * v_stride];
+            S.ks = ksp[(int64_t)pos * s_stride];
+            S.vs = vsp[(int64_t)pos * v_stride];
         }
     };
     // 8 int8 (bytes of .x, .y) as 8 fp16 (exact).
@@ -525,22 +542,40 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(AttnParams p, int start
         }
         return u32x4{o[0], o[1], o[2], o[3]};
     };
-    auto store_tile = [&](int b) {
+    auto store_tile = [&](int b, const Stage &S) {
 #pragma unroll
         for (int j = 0; j < NST; ++j) {
             const int id = tid + 256 * j;
-            const u32x4 kv = I8 ? i8_to_f16(kr[j]) : kr[j];
+            const u32x4 kv = I8 ? i8_to_f16(S.k[j]) : S.k[j];
             *reinterpret_cast<u32x4 *>(&kt[b][(id / KCH) * KROW + 8 * (id % KCH)]) = kv;
-            const u32x4 vv = I8 ? i8_to_f16(vr[j]) : vr[j];
-            const uint32_t wv[4] = {vv.x, vv.y, vv.z, vv.w};
-            const int vpos = id % kAttnTile, d0 = 8 * (id / kAttnTile);
+        }
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                vt[b][(d0 + e) * VROW + vpos] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+        for (int j = 0; j < NSV; ++j) {
+            const int id = tid + 256 * j;
+            if (id < NVU) {
+                const int q4 = id % (kAttnTile / 4), d0 = 8 * (id / (kAttnTile / 4));
+                uint32_t w[4][4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const u32x4 vv = I8 ? i8_to_f16(S.v[j][e]) : S.v[j][e];
+                    w[e][0] = vv.x; w[e][1] = vv.y; w[e][2] = vv.z; w[e][3] = vv.w;
+                }
+                // dim d0 + 2c + hh: halves hh of word c of positions 4 q4 .. + 3
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int sh = 16 * hh;
+                        const uint32_t lo = ((w[0][c] >> sh) & 0xFFFFu) | (((w[1][c] >> sh) & 0xFFFFu) << 16);
+                        const uint32_t hi = ((w[2][c] >> sh) & 0xFFFFu) | (((w[3][c] >> sh) & 0xFFFFu) << 16);
+                        *reinterpret_cast<u32x2 *>(&vt[b][(d0 + 2 * c + hh) * VROW + 4 * q4]) =
+                            u32x2{lo, hi};
+                    }
+            }
         }
         if (I8 && tid < kAttnTile) {
-            ksc[b][tid] = ksr;
-            vsc[b][tid] = vsr;
+            ksc[b][tid] = S.ks;
+            vsc[b][tid] = S.vs;
         }
     };
 
@@ -550,12 +585,15 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(AttnParams p, int start
     float m = -INFINITY, l = 0.0f;
     const float sl2 = p.scale * 1.4426950408889634f;  // scores in log2 units
 
-    load_tile(0);
-    store_tile(0);
+    // Tile it is in LDS buffer it & 1 during iteration it; tile it + 1 in
+    // registers, stored at its end; tile it + 2 loaded at its start.
+    Stage R0, R1;
+    load_tile(0, R0);
+    load_tile(kAttnTile, R1);
+    store_tile(0, R0);
     lds_sync();
-    for (int it = 0; it < n_tiles; ++it) {
-        const int b = it & 1, p0 = it * kAttnTile;
-        load_tile(p0 + kAttnTile);  // past the end: clamped re-reads, not stored
+    auto compute_tile = [&](int it, int b) {
+        const int p0 = it * kAttnTile;
         // S^T for the 4 sub-tiles of 16 positions.
         float sv[4][4];
 #pragma unroll
@@ -623,7 +661,16 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(AttnParams p, int start
                 o[dt] = mfma<RXQ4_DTYPE_F16>(a, u32x4{pl[ks2][0], pl[ks2][1], pl[ks2][2], pl[ks2][3]}, o[dt]);
             }
         }
-        if (it + 1 < n_tiles) store_tile(b ^ 1);  // uniform
+    };
+    for (int it = 0; it < n_tiles; it += 2) {
+        load_tile((it + 2) * kAttnTile, R0);  // past the end: clamped re-reads, not stored
+        compute_tile(it, 0);
+        if (it + 1 < n_tiles) store_tile(1, R1);  // uniform
+        lds_sync();
+        if (it + 1 >= n_tiles) break;
+        load_tile((it + 3) * kAttnTile, R1);
+        compute_tile(it + 1, 1);
+        if (it + 2 < n_tiles) store_tile(0, R0);
         lds_sync();
     }
     if (row_ok) {
