@@ -3,23 +3,16 @@
 // Replaces the reference's batched path (q4_gemm.cu:1297-1356 scalar kernel,
 // 1482-1636 mma.sync MMQ kernel, 1638-1740 host chunking).  The reference
 // re-streams W once per 20-token chunk; here every launch reads W once per
-// token tile of 16*TF tokens.
+// token tile of 128 tokens.
 //
 // Math: y[tok, row] = sum_k x[tok, k] * w[row, k] with w = d*sc*q - dmin*m
 // rounded once to fp32 and then (RNE) to the operand type of x (fp16 or
-// bf16), products accumulated in fp32 by v_mfma_f32_16x16x32_{f16,bf16}:
-//   src0 (16 x 32) = weight rows, lane l holds row l%16, k = 8*(l/16) .. +8
-//   src1 (32 x 16) = tokens,      lane l holds token l%16, same k
-//   dst  (16 x 16) lane l holds rows 4*(l/16) + r (r < 4) of token l%16.
-// A lane's 8 consecutive k of one sub-block are 8 quant bytes' low nibbles;
-// the same 8 bytes' high nibbles are the same k of the next sub-block, so one
-// 8-byte load feeds two MFMA k-steps.
-//
-// GEMM kernel: workgroup = 4 waves; wave w owns 64 weight rows (4 fragments)
-// and all 16*TF tokens of the workgroup's token tile.  The x tile (16*TF
-// tokens x 64 k) is staged in LDS, in a ring of 5 stages, and read by all 4 waves;
-// weights are dequantised straight into MFMA operand registers, so no wave
-// dequantises another wave's rows.  Flops per launch: 2*N*M*K.
+// bf16), products accumulated in fp32 by MFMA: v_mfma_f32_32x32x16 in the
+// GEMM (weight rows as src0, tokens as src1), v_mfma_f32_16x16x32 in the
+// small-batch kernel.  A lane's 8 consecutive k of one sub-block are 8 quant
+// bytes' low nibbles; the same 8 bytes' high nibbles are the same k of the
+// next sub-block, so one load feeds two MFMA k-steps.  Flops per launch:
+// 2*N*M*K.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -85,45 +78,53 @@ __device__ __forceinline__ GroupScales group_scales(u32x4 h, int il) {
 // ---------------------------------------------------------------------------
 // Tiled GEMM.
 //
-// Workgroup = 4 waves; wave w owns 64 weight rows (4 MFMA row fragments) and
-// all TM = 16*TF tokens of the workgroup tile (256 rows x TM tokens).  K is
-// walked in stages of 64 (one 32-byte quant group il of a super-block = two
-// sub-blocks = two MFMA k-steps):
-//   * activations: each stage's TM x 64 tile is copied global -> LDS by the
+// Workgroup = 8 waves, tile = 256 weight rows x 128 tokens; wave w owns 32
+// rows (one 32-row MFMA fragment) and all 128 tokens (four 32-token
+// fragments).  Two waves share each SIMD, so one wave's dequantisation
+// (VALU) issues while the other's MFMAs run: measured on gfx950, a single
+// wave hides only about half of its own VALU work behind its MFMAs, while a
+// second wave's VALU work hides almost entirely.  At ~160 VGPRs a wave fits
+// the 256-register budget of two waves per SIMD, and every weight is still
+// dequantised once per workgroup.  K is walked in stages of 64 (one 32-byte
+// quant group il of a super-block = two sub-blocks = four MFMA k-steps):
+//   * activations: each stage's 128 x 64 tile is copied global -> LDS by the
 //     gfx950 direct-to-LDS loads (buffer_load_dwordx4 ... lds) into a ring
 //     of 5 stage buffers, 4 stages ahead (issued right after the stage
 //     barrier, when every wave has finished reading the buffer being
 //     refilled).  Token t's 16-byte chunk c sits at position c ^ (t & 7) of
-//     the token's 128-byte row, so the fragment reads (16 tokens x 16 bytes
-//     per k-group) hit distinct banks;
-//   * weights: each lane loads the 8 quant bytes of its fragment row four
-//     stages ahead (the block header three stages ahead) and dequantises
-//     them straight into MFMA operand registers, one stage ahead of use: the
+//     the token's 128-byte row, so the fragment reads hit distinct banks;
+//   * B fragments (16 per wave per stage, 1 KB each) stream from LDS through
+//     a ring of 8 registers, read kLook MFMAs ahead (the last ones of a
+//     stage read the next stage's buffer).  That is 128 KB of LDS reads per
+//     stage and CU, a small part of the gfx950 LDS bandwidth;
+//   * weights: each lane loads the 16 quant bytes of its row four stages
+//     ahead (the block header three stages ahead) and dequantises them
+//     straight into MFMA operand registers, one stage ahead of use: the
 //     dequantisation of stage s+1 (VALU) is written between the MFMAs of
-//     stage s, one (fragment, half) per token fragment, so the two pipes
-//     overlap.  The prefetch depth is set by latency: with loads two stages
-//     ahead the kernel waited on memory at every stage;
-//   * per stage: wait until this stage's copies have landed (vmcnt), one
-//     workgroup barrier, refill the freed buffer, then 2 x 4 x TF MFMAs.
+//     stage s, a quarter operand per MFMA;
+//   * per stage: wait until the next stage's copies have landed (vmcnt),
+//     one workgroup barrier, refill the freed buffer, then 16 MFMAs.
 // The vmcnt bound is static: every stage issues the same loads (beyond the
 // last stage they repeat the last stage's addresses into buffers that are
-// never read), so the loads issued after stage s's copies are always its
-// own quant bytes, three later stages and one header batch: 3*kXLoads + 20.
+// never read), so the count of loads issued after a given stage's copies
+// is fixed.
+// Output: 16-bit tiles are staged through LDS as [token][row], so 32 lanes
+// write one token's 512 contiguous bytes (the MFMA layout, 4 rows of one
+// token per lane, would scatter 8-byte pieces over 32 tokens; measured 5.6 us
+// of 38.6 us for the m = 512 [11008 x 2048] GEMM written that way).
 // Split-K (splits > 1): each workgroup covers a range of super-blocks and
 // writes its fp32 tile to a workspace; a second launch (gemm_reduce_kernel)
 // adds the splits in split order and writes the output, so results do not
 // depend on scheduling.  The kernel boundary between the two launches is the
 // only synchronisation (no atomics, fences or spinning).
-constexpr int kGemmWaves = 4;
-constexpr int kRowsPerWave = 64;
-constexpr int kRowsPerWg = kGemmWaves * kRowsPerWave;
+constexpr int kRowsPerWg = 256;
 constexpr int kRing = 5;
 
 struct GemmParams {
     void *y;
     const uint8_t *w;
     const uint16_t *x;
-    float *ws;      // split-K partial tiles [tile][split][TF*4][256 threads] float4
+    float *ws;      // split-K partial tiles [tile][split][16][512 threads] float4
     int M, N, K, nb;
     int row_tiles, tok_tiles, splits, sb_per_split;
     int total_units, units_per_xcd;
@@ -162,26 +163,17 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// Output position of accumulator element i of (row fragment rf, token
-// fragment tf) held by lane `lane` of wave `wave` in tile (row_tile,
-// tok_tile): rows row..row+3 (j = i/4) of token tok.
-struct OutPos {
-    int row, tok;
-};
+constexpr int kW8Rows = 32;                       // weight rows per wave
+constexpr int kOutPitch = kRowsPerWg * 2 + 16;    // staged output: bytes per token
 
-template <int TF>
-__device__ __forceinline__ OutPos out_pos(int row_tile, int tok_tile, int wave, int lane, int rf,
-                                          int tf, int j) {
-    return OutPos{row_tile * kRowsPerWg + wave * kRowsPerWave + 32 * rf + 8 * j + 4 * (lane >> 5),
-                  tok_tile * 16 * TF + 32 * tf + (lane & 31)};
-}
-
-template <int XT, int YT, int TF>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
-    static_assert(TF == 8, "the stage body is written for 4 token fragments of 32");
-    constexpr int TM = 16 * TF;                // 128 tokens
-    constexpr int NT = TM / 32;                // 32-token fragments
-    constexpr int kXLoads = TM / 32;           // 1 KB direct-to-LDS loads per wave per stage
+template <int XT, int YT>
+__global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
+    constexpr int TM = 128;          // tokens per workgroup tile
+    constexpr int NT = TM / 32;      // 32-token fragments
+    constexpr int kXLoads = 2;       // 1 KB direct-to-LDS copies per wave per stage
+    constexpr int kQLoads = 1, kHLoads = 1;
+    constexpr int kLook = 6;         // B fragments are read kLook MFMAs before use
+    static_assert(TM * kOutPitch <= kRing * TM * 128, "staged output fits the ring");
     __shared__ __attribute__((aligned(1024))) uint8_t xs[kRing][TM * 128];
 
     const int L = blockIdx.x;
@@ -203,261 +195,236 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmParams p) {
     const int h = lane >> 5;    // k slot: bytes 16h .. 16h+15 of each 32-byte quant group
     const int K = p.K;
     const int64_t row_bytes = (int64_t)p.nb * kBlockBytes;
-    const int row_base = row_tile * kRowsPerWg + wave * kRowsPerWave;
+    const int row_base = row_tile * kRowsPerWg + wave * kW8Rows;
     const int tok_base = tok_tile * TM;
+    const uint8_t *wrow =
+        p.w + (int64_t)min(row_base + lr, p.M - 1) * row_bytes + sb0 * kBlockBytes;
 
-    const uint8_t *wrow[2];
-#pragma unroll
-    for (int rf = 0; rf < 2; ++rf)
-        wrow[rf] = p.w + (int64_t)min(row_base + 32 * rf + lr, p.M - 1) * row_bytes + sb0 * kBlockBytes;
-
-    // Direct-to-LDS copy of stage s (clamped to the last stage), as MUBUF
-    // buffer_load_dwordx4 ... lds over the workgroup's token rows (byte
-    // offsets < TM*K*2 <= 16 MiB).  The MUBUF form keeps the compiler's
-    // vmcnt bookkeeping for the register loads below exact; with the FLAT
-    // form (global_load_lds) it waits for vmcnt(0) at every use.
-    const int ctok = lane >> 3;                 // token within a 1 KB chunk
-    const int cpos = (lane & 7) ^ ctok;         // global 16-byte chunk this lane fetches
+    // Direct-to-LDS copies of the x tile: 16 chunks of 1 KB (8 tokens) per
+    // stage, chunks wave and wave + 8; chunk c of token t at c ^ (t & 7).
+    const int ctok = lane >> 3;
+    const int cpos = (lane & 7) ^ ctok;
     const __amdgpu_buffer_rsrc_t xrsrc =
         make_rsrc(p.x + (int64_t)tok_base * K, min(TM, p.N - tok_base) * K * 2);
     int xoff[kXLoads];
 #pragma unroll
     for (int i = 0; i < kXLoads; ++i) {
-        const int tok = min(8 * (wave + 4 * i) + ctok, p.N - 1 - tok_base);
+        const int tok = min(8 * (wave + 8 * i) + ctok, p.N - 1 - tok_base);
         xoff[i] = (tok * K + 8 * cpos) * 2;
     }
     auto issue_x = [&](int s) {
         const int st = min(s, n_stages - 1);
-        const int k0b = (sb0 * 4 + st) * 128;   // byte offset of the stage's 64 k
+        const int k0b = (sb0 * 4 + st) * 128;
 #pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const int jc = wave + 4 * i;        // 1 KB chunk = 8 tokens
-            buffer_to_lds16(xrsrc, &xs[s % kRing][jc * 1024], xoff[i] + k0b);
-        }
+        for (int i = 0; i < kXLoads; ++i)
+            buffer_to_lds16(xrsrc, &xs[s % kRing][(wave + 8 * i) * 1024], xoff[i] + k0b);
     };
-    // The lane's 16 quant bytes of stage s for both row fragments.
-    auto load_q = [&](int s, u32x4 *q) {
+    auto load_q = [&](int s) {
         const int st = min(s, n_stages - 1);
-        const int off = (st >> 2) * kBlockBytes + 16 + 32 * (st & 3) + 16 * h;
-#pragma unroll
-        for (int rf = 0; rf < 2; ++rf) q[rf] = load16(wrow[rf] + off);
+        return load16(wrow + (st >> 2) * kBlockBytes + 16 + 32 * (st & 3) + 16 * h);
     };
-    auto load_h = [&](int sbi, u32x4 *hd) {
-        const int sbc = min(sbi, nsb - 1);
-#pragma unroll
-        for (int rf = 0; rf < 2; ++rf) hd[rf] = load16(wrow[rf] + sbc * kBlockBytes);
-    };
+    auto load_h = [&](int sbi) { return load16(wrow + min(sbi, nsb - 1) * kBlockBytes); };
 
-    f32x16 acc[2][NT];
+    // Per-lane byte offset of B fragment (k-step k, token fragment 0) in a
+    // ring buffer: token lr, chunk c = (k/2)*4 + 2h + k%2 at c ^ (lr & 7);
+    // token fragment tf adds 4096*tf.
+    int boff[4];
 #pragma unroll
-    for (int rf = 0; rf < 2; ++rf)
-#pragma unroll
-        for (int tf = 0; tf < NT; ++tf) acc[rf][tf] = f32x16{};
-
-    u32x4 q[4][2];      // quant bytes of stages s .. s+3 (ring by s % 4), per row fragment
-    u32x4 hcur[2], hnext[2];
-    // Dequantised operands of stages s (a[s&1]) and s+1: [rf][k-step]
-    // with k-steps 0: low nibbles of bytes 0-7, 1: low nibbles of bytes
-    // 8-15, 2: high nibbles of bytes 0-7, 3: high nibbles of bytes 8-15 (the
-    // two sub-blocks of the quant group, 8 k each per lane).
-    u32x4 a[2][2][4];
-
-    auto dequant_stage = [&](const u32x4 *qs, const u32x4 *hd, int il, u32x4 (*out)[4]) {
-#pragma unroll
-        for (int rf = 0; rf < 2; ++rf) {
-            const GroupScales g = group_scales(hd[rf], il);
-            out[rf][0] = dequant8<XT>(qs[rf].x, qs[rf].y, false, g.lo, g.dm_lo);
-            out[rf][1] = dequant8<XT>(qs[rf].z, qs[rf].w, false, g.lo, g.dm_lo);
-            out[rf][2] = dequant8<XT>(qs[rf].x, qs[rf].y, true, g.hi, g.dm_hi);
-            out[rf][3] = dequant8<XT>(qs[rf].z, qs[rf].w, true, g.hi, g.dm_hi);
-        }
+    for (int k = 0; k < 4; ++k) {
+        const int c = (k >> 1) * 4 + 2 * h + (k & 1);
+        boff[k] = lr * 128 + ((c ^ (lr & 7)) << 4);
+    }
+    // MFMA n of a stage (n < 16): k-step n / 4, token fragment n % 4.
+    auto read_b = [&](int s, int n) {
+        return *reinterpret_cast<const u32x4 *>(&xs[s % kRing][4096 * (n & 3) + boff[n >> 2]]);
     };
 
-    // B fragments of token fragment tf of stage st, k-steps as for A: chunk
-    // (16 bytes = 8 k) 2h + step of the low sub-block, 4 + 2h + step of the
-    // high one, from ring buffer st % kRing (chunk c of token t sits at
-    // position c ^ (t & 7)).
-    auto read_b = [&](int st, int tf, u32x4 *b4) {
-        const uint8_t *xb = xs[st % kRing];
-        const int tt = 32 * tf + lr;
+    f32x16 acc[NT];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int c = (k >> 1) * 4 + 2 * h + (k & 1);
-            b4[k] = *reinterpret_cast<const u32x4 *>(xb + tt * 128 + ((c ^ (tt & 7)) << 4));
-        }
-    };
-    u32x4 bf[2][NT][4];  // B fragments of stages s (bf[s&1]) and s+1
+    for (int tf = 0; tf < NT; ++tf) acc[tf] = f32x16{};
 
-    // Prologue: the loads of stages 0..3 in the order the loop issues them
-    // (stage k's copies, its quant bytes, the header every 4th stage), the
-    // operands of stage 0, then its B fragments once its copies have landed.
-    // (sched_barrier pins the issue order the static vmcnt bounds count on.)
-    constexpr int kQLoads = 2, kHLoads = 2;
+    u32x4 q[4];          // quant bytes of stages s .. s+3 (ring by s % 4)
+    u32x4 hcur, hnext;   // block headers of the current / next super-block
+    u32x4 a[2][4];       // A operands of stages s (a[s&1]) and s+1, per k-step
+    u32x4 bq[8];         // B fragment ring, slot = MFMA sequence number % 8
+
+    // Prologue: loads of stages 0..3 in loop order, stage 0's operands, then
+    // its first kLook B fragments once its copies have landed.
     issue_x(0);
     __builtin_amdgcn_sched_barrier(0);
-    load_q(0, q[0]);
-    load_h(0, hcur);
+    q[0] = load_q(0);
+    hcur = load_h(0);
     issue_x(1);
     __builtin_amdgcn_sched_barrier(0);
-    load_q(1, q[1]);
+    q[1] = load_q(1);
     issue_x(2);
     __builtin_amdgcn_sched_barrier(0);
-    load_q(2, q[2]);
+    q[2] = load_q(2);
     issue_x(3);
     __builtin_amdgcn_sched_barrier(0);
-    load_q(3, q[3]);
-    dequant_stage(q[0], hcur, 0, a[0]);
-    // loads after stage 0's copies: 4 quant batches, 3 copy batches, 1 header batch
+    q[3] = load_q(3);
+    {
+        const GroupScales g = group_scales(hcur, 0);
+        a[0][0] = dequant8<XT>(q[0].x, q[0].y, false, g.lo, g.dm_lo);
+        a[0][1] = dequant8<XT>(q[0].z, q[0].w, false, g.lo, g.dm_lo);
+        a[0][2] = dequant8<XT>(q[0].x, q[0].y, true, g.hi, g.dm_hi);
+        a[0][3] = dequant8<XT>(q[0].z, q[0].w, true, g.hi, g.dm_hi);
+    }
     wait_vmcnt<3 * kXLoads + 4 * kQLoads + kHLoads>();
     lds_barrier();
 #pragma unroll
-    for (int tf = 0; tf < NT; ++tf) read_b(0, tf, bf[0][tf]);
+    for (int n = 0; n < kLook; ++n) bq[n] = read_b(0, n);
 
     for (int sbi = 0; sbi < nsb; ++sbi) {
 #pragma unroll
         for (int il = 0; il < 4; ++il) {
             const int s = 4 * sbi + il;
-            // Loads run 4 stages ahead: copies of stage s+4 into ring buffer
-            // (s+4) % 5, quant bytes of stage s+4 into q[il] (it held stage
-            // s, consumed during stage s-1), and at il == 0 the next
-            // super-block's headers.  Stage s's B fragments were read during
-            // stage s-1; this stage reads stage s+1's, so it waits for the
-            // copies of stage s+1: the loads issued after them are its quant
-            // bytes, two later stages and, unless il == 0, one header batch.
-            // After the barrier every wave has its stage s+1 copies and is
-            // past stage s-1, whose buffer is refilled.
+            // Wait for stage s+1's copies (read from MFMA 16 - kLook of this
+            // stage on); the loads issued after them are its quant bytes, two
+            // later stages and, unless il == 0, one header.  After the
+            // barrier every wave is past stage s-1, whose buffer is refilled.
             if (il == 0)
                 wait_vmcnt<2 * kXLoads + 3 * kQLoads>();
             else
                 wait_vmcnt<2 * kXLoads + 3 * kQLoads + kHLoads>();
             lds_barrier();
-            // The previous stage's reads of this stage's B fragments are
-            // long done; saying so up front keeps the compiler from waiting
-            // inside the MFMA stream on LDS reads issued in this stage (the
-            // LDS counter completes in order).
-            wait_lgkmcnt0();
             issue_x(s + 4);
             __builtin_amdgcn_sched_barrier(0);
-            load_q(s + 4, q[il]);
-            if (il == 0) load_h(sbi + 1, hnext);
+            q[il] = load_q(s + 4);
+            if (il == 0) hnext = load_h(sbi + 1);
 
-            // 32 MFMAs of stage s (k-step major: 8 independent accumulators
-            // between dependent ones), each followed by a quarter of one
-            // 8-weight operand of stage s+1 (the next quant group, or group 0
-            // of the next super-block; ~5 VALU ops) and, every other MFMA, one
-            // read of stage s+1's B fragments.  A wave issues in order, so
-            // this one-to-one pattern is what lets the VALU and LDS work run
-            // while the matrix core works on the preceding MFMA (32 cycles);
-            // sched_barrier keeps the order.
-            u32x4 (*acur)[4] = a[il & 1];
-            u32x4 (*anext)[4] = a[(il + 1) & 1];
-            const u32x4 *hn = il == 3 ? hnext : hcur;
-            const u32x4 *qn = q[(il + 1) & 3];
-            GroupScales gs[2];  // scales of stage s+1
+            // 16 MFMAs of stage s, each followed by a quarter of one 8-weight
+            // A operand of stage s+1 (~5 VALU ops) and one B fragment read
+            // kLook MFMAs ahead (into stage s+1 for the last kLook).
+            const u32x4 *acur = a[il & 1];
+            u32x4 *anext = a[(il + 1) & 1];
+            const u32x4 hn = il == 3 ? hnext : hcur;
+            const u32x4 qn = q[(il + 1) & 3];
+            const GroupScales gs = group_scales(hn, (il + 1) & 3);
+            uint32_t m0 = 0, m1 = 0, o0 = 0, o1 = 0, o2 = 0;
 #pragma unroll
-            for (int rf = 0; rf < 2; ++rf) gs[rf] = group_scales(hn[rf], (il + 1) & 3);
-            u32x4 (*bc)[4] = bf[il & 1];
-            u32x4 (*bn)[4] = bf[(il + 1) & 1];
-            const uint8_t *xnb = xs[(s + 1) % kRing];
-            uint32_t m0 = 0, m1 = 0, o0 = 0, o1 = 0, o2 = 0, o3 = 0;
-#pragma unroll
-            for (int idx = 0; idx < 32; ++idx) {
-                const int k = idx >> 3, tf = (idx >> 1) & 3, rf = idx & 1;
-                acc[rf][tf] = mfma32<XT>(acur[rf][k], bc[tf][k], acc[rf][tf]);
+            for (int n = 0; n < 16; ++n) {
+                const int k = n >> 2, tf = n & 3;
+                acc[tf] = mfma32<XT>(acur[k], bq[(16 * il + n) & 7], acc[tf]);
                 __builtin_amdgcn_sched_barrier(0);
-                // operand op = (rf2, k2) of stage s+1, piece idx % 4
-                const int op = idx >> 2, rf2 = op >> 2, k2 = op & 3, piece = idx & 3;
+                const int k2 = n >> 2, piece = n & 3;
                 const bool hi = k2 >= 2;
-                const float sc = hi ? gs[rf2].hi : gs[rf2].lo;
-                const float dm = hi ? gs[rf2].dm_hi : gs[rf2].dm_lo;
+                const float sc = hi ? gs.hi : gs.lo;
+                const float dm = hi ? gs.dm_hi : gs.dm_lo;
                 if (piece == 0) {
-                    m0 = nibble_bytes((k2 & 1) ? qn[rf2].z : qn[rf2].x, hi);
+                    m0 = nibble_bytes((k2 & 1) ? qn.z : qn.x, hi);
                     const f32x2 f = nibbles_f32<false>(m0);
                     o0 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
                 } else if (piece == 1) {
                     const f32x2 f = nibbles_f32<true>(m0);
                     o1 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
                 } else if (piece == 2) {
-                    m1 = nibble_bytes((k2 & 1) ? qn[rf2].w : qn[rf2].y, hi);
+                    m1 = nibble_bytes((k2 & 1) ? qn.w : qn.y, hi);
                     const f32x2 f = nibbles_f32<false>(m1);
                     o2 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
                 } else {
                     const f32x2 f = nibbles_f32<true>(m1);
-                    o3 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
-                    anext[rf2][k2] = u32x4{o0, o1, o2, o3};
+                    anext[k2] = u32x4{o0, o1, o2, pack2<XT>(sc * f[0] - dm, sc * f[1] - dm)};
                 }
-                if ((idx & 1) == 0) {
-                    // B fragment r = idx / 2 of stage s+1: token fragment r / 4, k-step r % 4
-                    const int r = idx >> 1, tf2 = r >> 2, kk = r & 3;
-                    const int tt = 32 * tf2 + lr;
-                    const int c = (kk >> 1) * 4 + 2 * h + (kk & 1);
-                    bn[tf2][kk] = *reinterpret_cast<const u32x4 *>(xnb + tt * 128 + ((c ^ (tt & 7)) << 4));
-                }
+                const int nr = n + kLook;
+                bq[(16 * il + nr) & 7] = nr < 16 ? read_b(s, nr) : read_b(s + 1, nr - 16);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (il == 3) {
-#pragma unroll
-                for (int rf = 0; rf < 2; ++rf) hcur[rf] = hnext[rf];
-            }
+            if (il == 3) hcur = hnext;
         }
     }
-    wait_vmcnt<0>();  // trailing clamped copies must land before the workgroup exits
+    // The trailing clamped copies and look-ahead reads must finish before
+    // the ring is reused or the workgroup exits.
+    wait_vmcnt<0>();
+    wait_lgkmcnt0();
 
     if (p.splits > 1) {
-        // partial tile: per thread 2 x NT x 4 float4 in (rf, tf, j) order
+        // partial tile: per thread NT x 4 float4 in (tf, j) order
         f32x4 *part = reinterpret_cast<f32x4 *>(p.ws) +
-                      ((int64_t)(tile * p.splits + split) * (8 * NT)) * 256 + tid;
+                      ((int64_t)(tile * p.splits + split) * (4 * NT)) * 512 + tid;
 #pragma unroll
-        for (int rf = 0; rf < 2; ++rf)
+        for (int tf = 0; tf < NT; ++tf)
 #pragma unroll
-            for (int tf = 0; tf < NT; ++tf)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    part[((rf * NT + tf) * 4 + j) * 256] =
-                        f32x4{acc[rf][tf][4 * j], acc[rf][tf][4 * j + 1], acc[rf][tf][4 * j + 2],
-                              acc[rf][tf][4 * j + 3]};
+            for (int j = 0; j < 4; ++j)
+                part[(tf * 4 + j) * 512] = f32x4{acc[tf][4 * j], acc[tf][4 * j + 1],
+                                                 acc[tf][4 * j + 2], acc[tf][4 * j + 3]};
         return;
     }
-    const bool vec_ok = (p.M & 3) == 0;
-#pragma unroll
-    for (int rf = 0; rf < 2; ++rf)
+    if (YT != RXQ4_DTYPE_F32 && (p.M & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) {
+        // Stage the tile as [token][256 rows] (16-bit) in the ring, then
+        // write 16 bytes per lane: 32 lanes cover one token's rows.
+        lds_barrier();  // every wave is done reading the ring
+        uint8_t *ot = &xs[0][0];
 #pragma unroll
         for (int tf = 0; tf < NT; ++tf)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const OutPos o = out_pos<TF>(row_tile, tok_tile, wave, lane, rf, tf, j);
-                if (o.tok >= p.N || o.row >= p.M) continue;
-                const int valid = min(4, p.M - o.row);
-                store4<YT>(p.y, (int64_t)o.tok * p.M + o.row,
-                           f32x4{acc[rf][tf][4 * j], acc[rf][tf][4 * j + 1], acc[rf][tf][4 * j + 2],
-                                 acc[rf][tf][4 * j + 3]},
-                           vec_ok && valid == 4, valid);
+                const int t = 32 * tf + lr, r = wave * kW8Rows + 8 * j + 4 * h;
+                uint32_t lo, hi;
+                if (YT == RXQ4_DTYPE_F16) {
+                    lo = f32_to_f16_bits(acc[tf][4 * j]) |
+                         ((uint32_t)f32_to_f16_bits(acc[tf][4 * j + 1]) << 16);
+                    hi = f32_to_f16_bits(acc[tf][4 * j + 2]) |
+                         ((uint32_t)f32_to_f16_bits(acc[tf][4 * j + 3]) << 16);
+                } else {
+                    lo = f32_to_bf16_bits(acc[tf][4 * j]) |
+                         ((uint32_t)f32_to_bf16_bits(acc[tf][4 * j + 1]) << 16);
+                    hi = f32_to_bf16_bits(acc[tf][4 * j + 2]) |
+                         ((uint32_t)f32_to_bf16_bits(acc[tf][4 * j + 3]) << 16);
+                }
+                *reinterpret_cast<u32x2 *>(ot + t * kOutPitch + r * 2) = u32x2{lo, hi};
             }
+        wait_lgkmcnt0();
+        lds_barrier();
+        const int row0 = row_tile * kRowsPerWg;
+#pragma unroll
+        for (int i = 0; i < TM * 32 / 512; ++i) {
+            const int id = tid + 512 * i, t = id >> 5, c = id & 31;
+            const int tok = tok_base + t, row = row0 + 8 * c;
+            if (tok < p.N && row < p.M)  // M % 8 == 0: all 8 rows are in range
+                *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p.y) + (int64_t)tok * p.M + row) =
+                    *reinterpret_cast<const u32x4 *>(ot + t * kOutPitch + c * 16);
+        }
+        return;
+    }
+    const bool vec_ok = (p.M & 3) == 0;
+#pragma unroll
+    for (int tf = 0; tf < NT; ++tf)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = row_base + 8 * j + 4 * h, tok = tok_base + 32 * tf + lr;
+            if (tok >= p.N || row >= p.M) continue;
+            const int valid = min(4, p.M - row);
+            store4<YT>(p.y, (int64_t)tok * p.M + row,
+                       f32x4{acc[tf][4 * j], acc[tf][4 * j + 1], acc[tf][4 * j + 2],
+                             acc[tf][4 * j + 3]},
+                       vec_ok && valid == 4, valid);
+        }
 }
 
-// Split-K reduction: block (tile, e) with e = (rf*NT + tf)*4 + j sums the
-// splits of one float4 of every thread of the tile in split order; thread
-// tid holds the positions of thread tid of the GEMM workgroups.
-template <int YT, int TF>
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p) {
-    constexpr int NT = TF / 2;
-    constexpr int E = 8 * NT;  // float4 per thread
+// Split-K reduction for gemm_kernel: block (tile, e), e = tf*4 + j, sums
+// float4 e of every thread of the tile over the splits in split order.
+template <int YT>
+__global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
+    constexpr int E = 16;  // float4 per thread
     const int tid = threadIdx.x;
     const int tile = blockIdx.x / E;
     const int e = blockIdx.x % E;
-    const int rf = e / (4 * NT), tf = (e / 4) % NT, j = e % 4;
+    const int tf = e / 4, j = e % 4;
     const int row_tile = tile / p.tok_tiles, tok_tile = tile % p.tok_tiles;
-    const OutPos o = out_pos<TF>(row_tile, tok_tile, tid >> 6, tid & 63, rf, tf, j);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int row = row_tile * kRowsPerWg + wave * kW8Rows + 8 * j + 4 * (lane >> 5);
+    const int tok = tok_tile * 128 + 32 * tf + (lane & 31);
     const f32x4 *src = reinterpret_cast<const f32x4 *>(p.ws) +
-                       ((int64_t)tile * p.splits * E + e) * 256 + tid;
+                       ((int64_t)tile * p.splits * E + e) * 512 + tid;
     f32x4 sum = src[0];
     for (int sp = 1; sp < p.splits; ++sp) {
-        const f32x4 v = src[(int64_t)sp * E * 256];
+        const f32x4 v = src[(int64_t)sp * E * 512];
         sum = f32x4{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
     }
-    if (o.tok >= p.N || o.row >= p.M) return;
-    const int valid = min(4, p.M - o.row);
-    store4<YT>(p.y, (int64_t)o.tok * p.M + o.row, sum, (p.M & 3) == 0 && valid == 4, valid);
+    if (tok >= p.N || row >= p.M) return;
+    const int valid = min(4, p.M - row);
+    store4<YT>(p.y, (int64_t)tok * p.M + row, sum, (p.M & 3) == 0 && valid == 4, valid);
 }
 
 // ---------------------------------------------------------------------------
@@ -606,8 +573,7 @@ static int env_or(const char *name, int dflt) {
 template <int XT, int YT>
 static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
                                 int K, hipStream_t st) {
-    constexpr int TF = 8;  // 128 tokens per workgroup
-    constexpr int TM = 16 * TF;
+    constexpr int TM = 128;  // tokens per workgroup tile
     GemmParams p{};
     p.y = y;
     p.w = w;
@@ -637,8 +603,8 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     }
     p.total_units = tiles * splits;
     p.units_per_xcd = (p.total_units + 7) / 8;
-    gemm_kernel<XT, YT, TF><<<8 * p.units_per_xcd, 256, 0, st>>>(p);
-    if (splits > 1) gemm_reduce_kernel<YT, TF><<<tiles * 4 * TF, 256, 0, st>>>(p);  // 4*TF = 8*NT float4 per thread
+    gemm_kernel<XT, YT><<<8 * p.units_per_xcd, 512, 0, st>>>(p);
+    if (splits > 1) gemm_reduce_kernel<YT><<<tiles * 16, 512, 0, st>>>(p);  // 16 float4 per thread
     return hipGetLastError();
 }
 
