@@ -89,17 +89,24 @@ __device__ __forceinline__ GroupScales group_scales(u32x4 h, int il) {
 // quant group il of a super-block = two sub-blocks = four MFMA k-steps):
 //   * activations: each stage's 128 x 64 tile is copied global -> LDS by the
 //     gfx950 direct-to-LDS loads (buffer_load_dwordx4 ... lds) into a ring
-//     of 5 stage buffers, 4 stages ahead (issued right after the stage
+//     of 4 stage buffers, 3 stages ahead (issued right after the stage
 //     barrier, when every wave has finished reading the buffer being
-//     refilled).  Token t's 16-byte chunk c sits at position c ^ (t & 7) of
-//     the token's 128-byte row, so the fragment reads hit distinct banks;
+//     refilled).  With 4 buffers and the stage loop unrolled by 4, every
+//     buffer address is a compile-time offset (a ring of 5 cost a divide by
+//     5 and an address add per LDS access).  Token t's 16-byte chunk c sits
+//     at position c ^ ((t >> 1) & 7) of the token's 128-byte row: a 16-lane
+//     group of a
+//     fragment read (16 consecutive tokens, one chunk each) then covers all
+//     64 LDS banks once (with c ^ (t & 7), tokens t and t + 8 collided;
+//     measured 2.9M bank-conflict cycles against 0.8M LDS-active cycles);
 //   * B fragments (16 per wave per stage, 1 KB each) stream from LDS through
 //     a ring of 8 registers, read kLook MFMAs ahead (the last ones of a
 //     stage read the next stage's buffer).  That is 128 KB of LDS reads per
 //     stage and CU, a small part of the gfx950 LDS bandwidth;
-//   * weights: each lane loads the 16 quant bytes of its row four stages
-//     ahead (the block header three stages ahead) and dequantises them
-//     straight into MFMA operand registers, one stage ahead of use: the
+//   * weights: each lane loads the 16 quant bytes of its row three stages
+//     ahead (the next block header at the start of a super-block) and
+//     dequantises them straight into MFMA operand registers, one stage
+//     ahead of use: the
 //     dequantisation of stage s+1 (VALU) is written between the MFMAs of
 //     stage s, a quarter operand per MFMA;
 //   * per stage: wait until the next stage's copies have landed (vmcnt),
@@ -118,7 +125,7 @@ __device__ __forceinline__ GroupScales group_scales(u32x4 h, int il) {
 // depend on scheduling.  The kernel boundary between the two launches is the
 // only synchronisation (no atomics, fences or spinning).
 constexpr int kRowsPerWg = 256;
-constexpr int kRing = 5;
+constexpr int kRing = 4;  // LDS stage buffers; stage s uses buffer s % 4
 
 struct GemmParams {
     void *y;
@@ -173,8 +180,10 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     constexpr int kXLoads = 2;       // 1 KB direct-to-LDS copies per wave per stage
     constexpr int kQLoads = 1, kHLoads = 1;
     constexpr int kLook = 6;         // B fragments are read kLook MFMAs before use
-    static_assert(TM * kOutPitch <= kRing * TM * 128, "staged output fits the ring");
-    __shared__ __attribute__((aligned(1024))) uint8_t xs[kRing][TM * 128];
+    constexpr int kBufBytes = TM * 128;                        // one stage of x
+    constexpr int kLdsBytes = TM * kOutPitch > kRing * kBufBytes ? TM * kOutPitch
+                                                                : kRing * kBufBytes;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
 
     const int L = blockIdx.x;
     const int V = (L % 8) * p.units_per_xcd + L / 8;  // consecutive units share an XCD
@@ -201,9 +210,10 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         p.w + (int64_t)min(row_base + lr, p.M - 1) * row_bytes + sb0 * kBlockBytes;
 
     // Direct-to-LDS copies of the x tile: 16 chunks of 1 KB (8 tokens) per
-    // stage, chunks wave and wave + 8; chunk c of token t at c ^ (t & 7).
+    // stage, chunks wave and wave + 8 (tokens 8*chunk + lane/8); chunk c of
+    // token t at c ^ ((t >> 1) & 7), and (t >> 1) & 7 = 4*(wave & 1) + lane/16.
     const int ctok = lane >> 3;
-    const int cpos = (lane & 7) ^ ctok;
+    const int cpos = (lane & 7) ^ ((4 * (wave & 1) + (ctok >> 1)) & 7);
     const __amdgpu_buffer_rsrc_t xrsrc =
         make_rsrc(p.x + (int64_t)tok_base * K, min(TM, p.N - tok_base) * K * 2);
     int xoff[kXLoads];
@@ -212,31 +222,32 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         const int tok = min(8 * (wave + 8 * i) + ctok, p.N - 1 - tok_base);
         xoff[i] = (tok * K + 8 * cpos) * 2;
     }
-    auto issue_x = [&](int s) {
-        const int st = min(s, n_stages - 1);
-        const int k0b = (sb0 * 4 + st) * 128;
+    // Stage s's copies (clamped to the last stage) into ring buffer s % 4;
+    // the stage's k offset is the wave-uniform soffset of the load.
+    auto issue_x = [&](int buf, int s) {
+        const int k0b = (sb0 * 4 + min(s, n_stages - 1)) * 128;
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i)
-            buffer_to_lds16(xrsrc, &xs[s % kRing][(wave + 8 * i) * 1024], xoff[i] + k0b);
+            buffer_to_lds16(xrsrc, lds + buf * kBufBytes + (wave + 8 * i) * 1024, xoff[i], k0b);
     };
-    auto load_q = [&](int s) {
-        const int st = min(s, n_stages - 1);
-        return load16(wrow + (st >> 2) * kBlockBytes + 16 + 32 * (st & 3) + 16 * h);
-    };
-    auto load_h = [&](int sbi) { return load16(wrow + min(sbi, nsb - 1) * kBlockBytes); };
+    // Quant bytes of group g of super-block sb (clamped to the last one, so
+    // loads past the end stay in the row); headers likewise.
+    const uint8_t *wq = wrow + 16 + 16 * h;
+    auto load_q = [&](int sb, int g) { return load16(wq + min(sb, nsb - 1) * kBlockBytes + 32 * g); };
+    auto load_h = [&](int sb) { return load16(wrow + min(sb, nsb - 1) * kBlockBytes); };
 
     // Per-lane byte offset of B fragment (k-step k, token fragment 0) in a
-    // ring buffer: token lr, chunk c = (k/2)*4 + 2h + k%2 at c ^ (lr & 7);
-    // token fragment tf adds 4096*tf.
+    // ring buffer: token lr, chunk c = (k/2)*4 + 2h + k%2 at
+    // c ^ ((lr >> 1) & 7); token fragment tf adds 4096*tf.
     int boff[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int c = (k >> 1) * 4 + 2 * h + (k & 1);
-        boff[k] = lr * 128 + ((c ^ (lr & 7)) << 4);
+        boff[k] = lr * 128 + ((c ^ ((lr >> 1) & 7)) << 4);
     }
     // MFMA n of a stage (n < 16): k-step n / 4, token fragment n % 4.
-    auto read_b = [&](int s, int n) {
-        return *reinterpret_cast<const u32x4 *>(&xs[s % kRing][4096 * (n & 3) + boff[n >> 2]]);
+    auto read_b = [&](int buf, int n) {
+        return *reinterpret_cast<const u32x4 *>(lds + buf * kBufBytes + 4096 * (n & 3) + boff[n >> 2]);
     };
 
     f32x16 acc[NT];
@@ -248,21 +259,18 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     u32x4 a[2][4];       // A operands of stages s (a[s&1]) and s+1, per k-step
     u32x4 bq[8];         // B fragment ring, slot = MFMA sequence number % 8
 
-    // Prologue: loads of stages 0..3 in loop order, stage 0's operands, then
+    // Prologue: loads of stages 0..2 in loop order, stage 0's operands, then
     // its first kLook B fragments once its copies have landed.
-    issue_x(0);
+    issue_x(0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    q[0] = load_q(0);
+    q[0] = load_q(0, 0);
     hcur = load_h(0);
-    issue_x(1);
+    issue_x(1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    q[1] = load_q(1);
-    issue_x(2);
+    q[1] = load_q(0, 1);
+    issue_x(2, 2);
     __builtin_amdgcn_sched_barrier(0);
-    q[2] = load_q(2);
-    issue_x(3);
-    __builtin_amdgcn_sched_barrier(0);
-    q[3] = load_q(3);
+    q[2] = load_q(0, 2);
     {
         const GroupScales g = group_scales(hcur, 0);
         a[0][0] = dequant8<XT>(q[0].x, q[0].y, false, g.lo, g.dm_lo);
@@ -270,7 +278,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         a[0][2] = dequant8<XT>(q[0].x, q[0].y, true, g.hi, g.dm_hi);
         a[0][3] = dequant8<XT>(q[0].z, q[0].w, true, g.hi, g.dm_hi);
     }
-    wait_vmcnt<3 * kXLoads + 4 * kQLoads + kHLoads>();
+    wait_vmcnt<2 * kXLoads + 3 * kQLoads + kHLoads>();
     lds_barrier();
 #pragma unroll
     for (int n = 0; n < kLook; ++n) bq[n] = read_b(0, n);
@@ -279,18 +287,21 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int il = 0; il < 4; ++il) {
             const int s = 4 * sbi + il;
-            // Wait for stage s+1's copies (read from MFMA 16 - kLook of this
-            // stage on); the loads issued after them are its quant bytes, two
-            // later stages and, unless il == 0, one header.  After the
+            // Copies and quant bytes run 3 stages ahead (ring buffer and q
+            // slot (s+3) % 4 held stage s-1, finished during stage s-1), the
+            // next super-block's header is issued at il == 0.  Wait for stage
+            // s+1's copies (read from MFMA 16 - kLook of this stage on): the
+            // loads issued after them are its quant bytes, stage s+2's copies
+            // and quant bytes and, at il == 1 and 2, one header.  After the
             // barrier every wave is past stage s-1, whose buffer is refilled.
-            if (il == 0)
-                wait_vmcnt<2 * kXLoads + 3 * kQLoads>();
+            if (il == 1 || il == 2)
+                wait_vmcnt<kXLoads + 2 * kQLoads + kHLoads>();
             else
-                wait_vmcnt<2 * kXLoads + 3 * kQLoads + kHLoads>();
+                wait_vmcnt<kXLoads + 2 * kQLoads>();
             lds_barrier();
-            issue_x(s + 4);
+            issue_x((il + 3) & 3, s + 3);
             __builtin_amdgcn_sched_barrier(0);
-            q[il] = load_q(s + 4);
+            q[(il + 3) & 3] = load_q(sbi + ((il + 3) >> 2), (il + 3) & 3);
             if (il == 0) hnext = load_h(sbi + 1);
 
             // 16 MFMAs of stage s, each followed by a quarter of one 8-weight
@@ -327,7 +338,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
                     anext[k2] = u32x4{o0, o1, o2, pack2<XT>(sc * f[0] - dm, sc * f[1] - dm)};
                 }
                 const int nr = n + kLook;
-                bq[(16 * il + nr) & 7] = nr < 16 ? read_b(s, nr) : read_b(s + 1, nr - 16);
+                bq[(16 * il + nr) & 7] = nr < 16 ? read_b(il, nr) : read_b((il + 1) & 3, nr - 16);
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (il == 3) hcur = hnext;
@@ -354,7 +365,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         // Stage the tile as [token][256 rows] (16-bit) in the ring, then
         // write 16 bytes per lane: 32 lanes cover one token's rows.
         lds_barrier();  // every wave is done reading the ring
-        uint8_t *ot = &xs[0][0];
+        uint8_t *ot = lds;
 #pragma unroll
         for (int tf = 0; tf < NT; ++tf)
 #pragma unroll

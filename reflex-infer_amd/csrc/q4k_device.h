@@ -111,11 +111,12 @@ __device__ __forceinline__ u32x2 buffer_load8(__amdgpu_buffer_rsrc_t rsrc, int v
     return __builtin_amdgcn_raw_buffer_load_b64(rsrc, voffset, 0, 0);
 }
 
-// 16 bytes per lane, global (rsrc + voffset) -> LDS at lds + 16 * lane.
+// 16 bytes per lane, global (rsrc + voffset + soffset) -> LDS at
+// lds + 16 * lane; soffset is wave-uniform.
 __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds,
-                                                int voffset) {
+                                                int voffset, int soffset = 0) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rsrc, (void __attribute__((address_space(3))) *)lds, 16, voffset, 0, 0, 0);
+        rsrc, (void __attribute__((address_space(3))) *)lds, 16, voffset, soffset, 0, 0);
 }
 
 // s_waitcnt lgkmcnt(0) (vmcnt and expcnt untouched).
