@@ -173,12 +173,236 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 constexpr int kW8Rows = 32;                       // weight rows per wave
 constexpr int kOutPitch = kRowsPerWg * 2 + 16;    // staged output: bytes per token
 
-template <int XT, int YT>
+// ---------------------------------------------------------------------------
+// Weight formats of the GEMM.  A stage is 64 weights of every row; lane
+// (row lr, half h) dequantises 32 of them into four 8-weight MFMA operands
+// (k-steps kk = 0..3), a quarter operand ("piece" p = 0..3, weights 2p and
+// 2p+1) per MFMA of the previous stage.  chunk(kk, h) is the 8-element x
+// chunk (0..7) of the stage that k-step kk of half h multiplies; the stage's
+// x elements are k0 + stage_elem(st) + chunk_elem(c) + 0..7.  Every weight is
+// rounded once to fp32 (one fma of the reference's factors) and then to the
+// x type.
+template <int T>
+struct GemmFmt;
+
+// Q4_K (144 B): stage g of a super-block = quant group g (sub-blocks 2g and
+// 2g+1); half h holds qs bytes 16h..16h+15 of the group, k-step kk the low
+// (kk < 2) or high nibbles of bytes 8*(kk & 1)..+7.  Nibbles convert through
+// the FP8 trick (dequant4): w = (512*d*sc) * (q * 2^-9) - dmin*m.
+template <>
+struct GemmFmt<12> {
+    static constexpr int kBytes = 144, kQLoads = 1, kHLoads = 1;
+    struct Stage {
+        u32x4 q;
+    };
+    struct Sb {
+        u32x4 h;
+    };
+    struct Loader {
+        const uint8_t *row;  // the lane's row at the first super-block
+        int nsb, h;
+        // super-block indices clamp to the last one: loads past the end stay in the row
+        __device__ Stage stage(int sb, int g) const {
+            return {load16(row + min(sb, nsb - 1) * kBytes + 16 + 32 * g + 16 * h)};
+        }
+        __device__ Sb header(int sb) const { return {load16(row + min(sb, nsb - 1) * kBytes)}; }
+    };
+    using Scales = GroupScales;
+    __device__ static Scales scales(const Sb &b, int g) { return group_scales(b.h, g); }
+    __device__ static void prepare(Stage &, const Sb &) {}
+    __device__ static int chunk(int kk, int h) { return (kk >> 1) * 4 + 2 * h + (kk & 1); }
+    __device__ static int chunk_elem(int c) { return 8 * c; }
+    __device__ static int stage_elem(int st) { return 64 * st; }
+    struct Piece {
+        uint32_t m, o[3];
+    };
+    template <int XT>
+    __device__ static void piece(int kk, int p, int g, const Stage &s, const Sb &, const Scales &gs,
+                                 Piece &st, u32x4 &out) {
+        const bool hi = kk >= 2;
+        const float sc = hi ? gs.hi : gs.lo;
+        const float dm = hi ? gs.dm_hi : gs.dm_lo;
+        if ((p & 1) == 0) st.m = nibble_bytes(p == 0 ? ((kk & 1) ? s.q.z : s.q.x)
+                                                     : ((kk & 1) ? s.q.w : s.q.y), hi);
+        const f32x2 f = (p & 1) ? nibbles_f32<true>(st.m) : nibbles_f32<false>(st.m);
+        const uint32_t o = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
+        if (p < 3) st.o[p] = o;
+        else out = u32x4{st.o[0], st.o[1], st.o[2], o};
+    }
+};
+
+// Byte b (0..3) of v as fp32 (v_cvt_f32_ubyte<b>).
+__device__ __forceinline__ float byte_f32(uint32_t v, int b) {
+    return (float)((v >> (8 * b)) & 0xFFu);
+}
+
+// Q5_K (176 B): the Q4_K layout of qs (@48) and scales, plus the fifth bit
+// 2g + hi of qh[l] (@16); half h keeps qh bytes 16h..16h+15 with the
+// super-block header.  q = nibble | bit << 4 (0..31) converts with
+// v_cvt_f32_ubyte: w = (d*sc) * q - dmin*m.
+template <>
+struct GemmFmt<13> {
+    static constexpr int kBytes = 176, kQLoads = 1, kHLoads = 2;
+    struct Stage {
+        u32x4 q;
+    };
+    struct Sb {
+        u32x4 h, qh;
+    };
+    struct Loader {
+        const uint8_t *row;
+        int nsb, h;
+        __device__ Stage stage(int sb, int g) const {
+            return {load16(row + min(sb, nsb - 1) * kBytes + 48 + 32 * g + 16 * h)};
+        }
+        __device__ Sb header(int sb) const {
+            const uint8_t *b = row + min(sb, nsb - 1) * kBytes;
+            return {load16(b), load16(b + 16 + 16 * h)};
+        }
+    };
+    struct Scales {
+        float lo, hi, dm_lo, dm_hi;
+    };
+    __device__ static Scales scales(const Sb &b, int g) {
+        const float d = f16_bits_to_f32(b.h.x & 0xFFFFu), dmin = f16_bits_to_f32(b.h.x >> 16);
+        uint32_t sc, mn;
+        scale_pair(b.h.y, b.h.z, b.h.w, g, &sc, &mn);
+        return Scales{d * (float)(sc & 0xFFu), d * (float)(sc >> 8), dmin * (float)(mn & 0xFFu),
+                      dmin * (float)(mn >> 8)};
+    }
+    __device__ static void prepare(Stage &, const Sb &) {}
+    __device__ static int chunk(int kk, int h) { return GemmFmt<12>::chunk(kk, h); }
+    __device__ static int chunk_elem(int c) { return 8 * c; }
+    __device__ static int stage_elem(int st) { return 64 * st; }
+    struct Piece {
+        uint32_t m, o[3];
+    };
+    template <int XT>
+    __device__ static void piece(int kk, int p, int g, const Stage &s, const Sb &b,
+                                 const Scales &gs, Piece &st, u32x4 &out) {
+        const int hi = kk >> 1, dw = 2 * (kk & 1) + (p >> 1);
+        const float sc = hi ? gs.hi : gs.lo;
+        const float dm = hi ? gs.dm_hi : gs.dm_lo;
+        if ((p & 1) == 0) {
+            const uint32_t lo = (s.q[dw] >> (4 * hi)) & 0x0F0F0F0Fu;
+            st.m = lo | (((b.qh[dw] >> (2 * g + hi)) & 0x01010101u) << 4);
+        }
+        const int e = 2 * (p & 1);
+        const uint32_t o = pack2<XT>(sc * byte_f32(st.m, e) - dm, sc * byte_f32(st.m, e + 1) - dm);
+        if (p < 3) st.o[p] = o;
+        else out = u32x4{st.o[0], st.o[1], st.o[2], o};
+    }
+};
+
+// Q6_K (210 B, only 2-byte aligned): stage g of a super-block = half
+// n = g / 2 (128 weights), run lh = g % 2; its 64 weights are
+// 128n + 32m + 16lh + (0..15) for m = 0..3, k-step kk = m, and half h takes
+// l = 16lh + 8h + (0..7): ql bytes 64n + 16lh + 8h (m = 0 low nibbles, m = 2
+// high) and 64n + 32 + 16lh + 8h (m = 1, 3), qh bytes 128 + 32n + 16lh + 8h
+// (bits 2m, 2m+1), scale sc[8n + 2m + lh].  The fields are read with
+// dword-aligned buffer loads (bounded to the wave's rows: rows past the
+// matrix read zeros) and realigned by the lane's byte offset r (0 or 2),
+// fixed per super-block.  q (0..63) converts with v_cvt_f32_ubyte:
+// w = (d*sc) * q - 32*(d*sc) = d*sc*(q - 32) exactly as the reference.
+template <>
+struct GemmFmt<14> {
+    static constexpr int kBytes = 210, kQLoads = 3, kHLoads = 3;
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+    struct Stage {
+        u32x3 a, b, qh;    // raw dwords of ql (m = 0, 2), ql (m = 1, 3), qh
+        u32x2 ra, rb, rh;  // realigned 8 bytes of each (prepare)
+    };
+    struct Sb {
+        u32x4 sc;      // raw dwords of the 16 scale bytes (+ 4 below)
+        uint32_t sce;  // dword after sc
+        uint32_t d;    // fp16 d in the low half
+        int r;         // byte offset of the lane's block fields in the dwords
+    };
+    struct Loader {
+        __amdgpu_buffer_rsrc_t rs;  // the wave's rows from the first super-block, dword-aligned
+        int base;                   // byte offset of the lane's row in rs
+        int nsb, h;
+        __device__ int block(int sb) const { return base + min(sb, nsb - 1) * kBytes; }
+        __device__ Stage stage(int sb, int g) const {
+            const int o = block(sb), n = g >> 1, lh = g & 1, f = 16 * lh + 8 * h;
+            const int oa = (o + 64 * n + f) & ~3, ob = (o + 64 * n + 32 + f) & ~3,
+                      oh = (o + 128 + 32 * n + f) & ~3;
+            Stage s;
+            s.a = __builtin_amdgcn_raw_buffer_load_b96(rs, oa, 0, 0);
+            s.b = __builtin_amdgcn_raw_buffer_load_b96(rs, ob, 0, 0);
+            s.qh = __builtin_amdgcn_raw_buffer_load_b96(rs, oh, 0, 0);
+            return s;
+        }
+        __device__ Sb header(int sb) const {
+            const int o = block(sb);
+            Sb b;
+            b.sc = buffer_load16(rs, (o + 192) & ~3);
+            b.sce = buffer_load4(rs, ((o + 192) & ~3) + 16);
+            // 2-byte load: a dword could reach past the last block
+            b.d = __builtin_amdgcn_raw_buffer_load_b16(rs, o + 208, 0, 0);
+            b.r = o & 3;
+            return b;
+        }
+    };
+    struct Scales {
+        float ds[4], off[4];
+    };
+    __device__ static Scales scales(const Sb &b, int g) {
+        const int n = g >> 1, lh = g & 1;
+        const float d = f16_bits_to_f32(b.d & 0xFFFFu);
+        const uint32_t w[5] = {b.sc.x, b.sc.y, b.sc.z, b.sc.w, b.sce};
+        // scale bytes 8n .. 8n+7: realigned dwords 2n, 2n+1
+        const uint32_t S[2] = {align_bytes(w[2 * n + 1], w[2 * n], b.r),
+                               align_bytes(w[2 * n + 2], w[2 * n + 1], b.r)};
+        Scales s;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int sh = 8 * (2 * (m & 1) + lh);  // byte 2m + lh of the 8
+            s.ds[m] = d * (float)((int)(S[m >> 1] << (24 - sh)) >> 24);
+            s.off[m] = -32.0f * s.ds[m];
+        }
+        return s;
+    }
+    __device__ static u32x2 realign8(u32x3 v, int r) {
+        return u32x2{align_bytes(v.y, v.x, r), align_bytes(v.z, v.y, r)};
+    }
+    __device__ static void prepare(Stage &s, const Sb &b) {
+        s.ra = realign8(s.a, b.r);
+        s.rb = realign8(s.b, b.r);
+        s.rh = realign8(s.qh, b.r);
+    }
+    __device__ static int chunk(int kk, int h) { return 2 * kk + h; }
+    __device__ static int chunk_elem(int c) { return 32 * (c >> 1) + 8 * (c & 1); }
+    __device__ static int stage_elem(int st) {
+        return 256 * (st >> 2) + 128 * ((st >> 1) & 1) + 16 * (st & 1);
+    }
+    struct Piece {
+        uint32_t m, o[3];
+    };
+    template <int XT>
+    __device__ static void piece(int kk, int p, int, const Stage &s, const Sb &, const Scales &gs,
+                                 Piece &st, u32x4 &out) {
+        const int dw = p >> 1;
+        if ((p & 1) == 0) {
+            const uint32_t ql = (kk & 1) ? s.rb[dw] : s.ra[dw];
+            const uint32_t lo = (ql >> (4 * (kk >> 1))) & 0x0F0F0F0Fu;
+            st.m = lo | (((s.rh[dw] >> (2 * kk)) & 0x03030303u) << 4);
+        }
+        const int e = 2 * (p & 1);
+        const float ds = gs.ds[kk], off = gs.off[kk];
+        const uint32_t o = pack2<XT>(ds * byte_f32(st.m, e) + off, ds * byte_f32(st.m, e + 1) + off);
+        if (p < 3) st.o[p] = o;
+        else out = u32x4{st.o[0], st.o[1], st.o[2], o};
+    }
+};
+
+template <int T, int XT, int YT>
 __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
+    using F = GemmFmt<T>;
     constexpr int TM = 128;          // tokens per workgroup tile
     constexpr int NT = TM / 32;      // 32-token fragments
     constexpr int kXLoads = 2;       // 1 KB direct-to-LDS copies per wave per stage
-    constexpr int kQLoads = 1, kHLoads = 1;
+    constexpr int kQLoads = F::kQLoads, kHLoads = F::kHLoads;
     constexpr int kLook = 6;         // B fragments are read kLook MFMAs before use
     constexpr int kBufBytes = TM * 128;                        // one stage of x
     constexpr int kLdsBytes = TM * kOutPitch > kRing * kBufBytes ? TM * kOutPitch
@@ -201,13 +425,27 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 31;   // row (A) / token (B) within a 32-fragment
-    const int h = lane >> 5;    // k slot: bytes 16h .. 16h+15 of each 32-byte quant group
+    const int h = lane >> 5;    // half of the stage's weights of the row
     const int K = p.K;
-    const int64_t row_bytes = (int64_t)p.nb * kBlockBytes;
+    const int64_t row_bytes = (int64_t)p.nb * F::kBytes;
     const int row_base = row_tile * kRowsPerWg + wave * kW8Rows;
     const int tok_base = tok_tile * TM;
-    const uint8_t *wrow =
-        p.w + (int64_t)min(row_base + lr, p.M - 1) * row_bytes + sb0 * kBlockBytes;
+
+    typename F::Loader ld;
+    if constexpr (T == 14) {
+        // buffer resource over the wave's rows (none past the matrix) from
+        // super-block sb0, based at the dword at or below its first byte
+        const uint8_t *first = p.w + (int64_t)row_base * row_bytes + sb0 * F::kBytes;
+        const int ex = (int)(reinterpret_cast<uintptr_t>(first) & 3);
+        const int rows = max(0, min(kW8Rows, p.M - row_base));
+        const int64_t span = rows ? (rows - 1) * row_bytes + (p.nb - sb0) * F::kBytes : 0;
+        ld.rs = make_rsrc(first - ex, (int)(span + ex));
+        ld.base = (int)(lr * row_bytes) + ex;
+    } else {
+        ld.row = p.w + (int64_t)min(row_base + lr, p.M - 1) * row_bytes + sb0 * F::kBytes;
+    }
+    ld.nsb = nsb;
+    ld.h = h;
 
     // Direct-to-LDS copies of the x tile: 16 chunks of 1 KB (8 tokens) per
     // stage, chunks wave and wave + 8 (tokens 8*chunk + lane/8); chunk c of
@@ -220,31 +458,23 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < kXLoads; ++i) {
         const int tok = min(8 * (wave + 8 * i) + ctok, p.N - 1 - tok_base);
-        xoff[i] = (tok * K + 8 * cpos) * 2;
+        xoff[i] = (tok * K + F::chunk_elem(cpos)) * 2;
     }
     // Stage s's copies (clamped to the last stage) into ring buffer s % 4;
     // the stage's k offset is the wave-uniform soffset of the load.
     auto issue_x = [&](int buf, int s) {
-        const int k0b = (sb0 * 4 + min(s, n_stages - 1)) * 128;
+        const int k0b = (sb0 * 256 + F::stage_elem(min(s, n_stages - 1))) * 2;
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i)
             buffer_to_lds16(xrsrc, lds + buf * kBufBytes + (wave + 8 * i) * 1024, xoff[i], k0b);
     };
-    // Quant bytes of group g of super-block sb (clamped to the last one, so
-    // loads past the end stay in the row); headers likewise.
-    const uint8_t *wq = wrow + 16 + 16 * h;
-    auto load_q = [&](int sb, int g) { return load16(wq + min(sb, nsb - 1) * kBlockBytes + 32 * g); };
-    auto load_h = [&](int sb) { return load16(wrow + min(sb, nsb - 1) * kBlockBytes); };
 
     // Per-lane byte offset of B fragment (k-step k, token fragment 0) in a
-    // ring buffer: token lr, chunk c = (k/2)*4 + 2h + k%2 at
-    // c ^ ((lr >> 1) & 7); token fragment tf adds 4096*tf.
+    // ring buffer: token lr, chunk c = chunk(k, h) at c ^ ((lr >> 1) & 7);
+    // token fragment tf adds 4096*tf.
     int boff[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int c = (k >> 1) * 4 + 2 * h + (k & 1);
-        boff[k] = lr * 128 + ((c ^ ((lr >> 1) & 7)) << 4);
-    }
+    for (int k = 0; k < 4; ++k) boff[k] = lr * 128 + ((F::chunk(k, h) ^ ((lr >> 1) & 7)) << 4);
     // MFMA n of a stage (n < 16): k-step n / 4, token fragment n % 4.
     auto read_b = [&](int buf, int n) {
         return *reinterpret_cast<const u32x4 *>(lds + buf * kBufBytes + 4096 * (n & 3) + boff[n >> 2]);
@@ -254,29 +484,30 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int tf = 0; tf < NT; ++tf) acc[tf] = f32x16{};
 
-    u32x4 q[4];          // quant bytes of stages s .. s+3 (ring by s % 4)
-    u32x4 hcur, hnext;   // block headers of the current / next super-block
-    u32x4 a[2][4];       // A operands of stages s (a[s&1]) and s+1, per k-step
-    u32x4 bq[8];         // B fragment ring, slot = MFMA sequence number % 8
+    typename F::Stage q[4];   // weights of stages s .. s+3 (ring by s % 4)
+    typename F::Sb hcur, hnext;  // per-super-block data, current and next
+    u32x4 a[2][4];            // A operands of stages s (a[s&1]) and s+1, per k-step
+    u32x4 bq[8];              // B fragment ring, slot = MFMA sequence number % 8
 
     // Prologue: loads of stages 0..2 in loop order, stage 0's operands, then
     // its first kLook B fragments once its copies have landed.
     issue_x(0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    q[0] = load_q(0, 0);
-    hcur = load_h(0);
+    q[0] = ld.stage(0, 0);
+    hcur = ld.header(0);
     issue_x(1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    q[1] = load_q(0, 1);
+    q[1] = ld.stage(0, 1);
     issue_x(2, 2);
     __builtin_amdgcn_sched_barrier(0);
-    q[2] = load_q(0, 2);
+    q[2] = ld.stage(0, 2);
     {
-        const GroupScales g = group_scales(hcur, 0);
-        a[0][0] = dequant8<XT>(q[0].x, q[0].y, false, g.lo, g.dm_lo);
-        a[0][1] = dequant8<XT>(q[0].z, q[0].w, false, g.lo, g.dm_lo);
-        a[0][2] = dequant8<XT>(q[0].x, q[0].y, true, g.hi, g.dm_hi);
-        a[0][3] = dequant8<XT>(q[0].z, q[0].w, true, g.hi, g.dm_hi);
+        F::prepare(q[0], hcur);
+        const typename F::Scales g = F::scales(hcur, 0);
+        typename F::Piece pc;
+#pragma unroll
+        for (int n = 0; n < 16; ++n)
+            F::template piece<XT>(n >> 2, n & 3, 0, q[0], hcur, g, pc, a[0][n >> 2]);
     }
     wait_vmcnt<2 * kXLoads + 3 * kQLoads + kHLoads>();
     lds_barrier();
@@ -287,12 +518,12 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int il = 0; il < 4; ++il) {
             const int s = 4 * sbi + il;
-            // Copies and quant bytes run 3 stages ahead (ring buffer and q
-            // slot (s+3) % 4 held stage s-1, finished during stage s-1), the
-            // next super-block's header is issued at il == 0.  Wait for stage
-            // s+1's copies (read from MFMA 16 - kLook of this stage on): the
-            // loads issued after them are its quant bytes, stage s+2's copies
-            // and quant bytes and, at il == 1 and 2, one header.  After the
+            // Copies and weights run 3 stages ahead (ring buffer and q slot
+            // (s+3) % 4 held stage s-1, finished during stage s-1), the next
+            // super-block's data is issued at il == 0.  Wait for stage s+1's
+            // copies (read from MFMA 16 - kLook of this stage on): the loads
+            // issued after them are its weights, stage s+2's copies and
+            // weights and, at il == 1 and 2, the super-block data.  After the
             // barrier every wave is past stage s-1, whose buffer is refilled.
             if (il == 1 || il == 2)
                 wait_vmcnt<kXLoads + 2 * kQLoads + kHLoads>();
@@ -301,43 +532,26 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
             lds_barrier();
             issue_x((il + 3) & 3, s + 3);
             __builtin_amdgcn_sched_barrier(0);
-            q[(il + 3) & 3] = load_q(sbi + ((il + 3) >> 2), (il + 3) & 3);
-            if (il == 0) hnext = load_h(sbi + 1);
+            q[(il + 3) & 3] = ld.stage(sbi + ((il + 3) >> 2), (il + 3) & 3);
+            if (il == 0) hnext = ld.header(sbi + 1);
 
             // 16 MFMAs of stage s, each followed by a quarter of one 8-weight
-            // A operand of stage s+1 (~5 VALU ops) and one B fragment read
-            // kLook MFMAs ahead (into stage s+1 for the last kLook).  The
-            // compiler's own interleave of this stream measured 1-3% faster
-            // than one pinned with sched_barrier.
+            // A operand of stage s+1 and one B fragment read kLook MFMAs
+            // ahead (into stage s+1 for the last kLook).  The compiler's own
+            // interleave of this stream measured 1-3% faster than one pinned
+            // with sched_barrier.
             const u32x4 *acur = a[il & 1];
             u32x4 *anext = a[(il + 1) & 1];
-            const u32x4 hn = il == 3 ? hnext : hcur;
-            const u32x4 qn = q[(il + 1) & 3];
-            const GroupScales gs = group_scales(hn, (il + 1) & 3);
-            uint32_t m0 = 0, m1 = 0, o0 = 0, o1 = 0, o2 = 0;
+            const typename F::Sb &hn = il == 3 ? hnext : hcur;
+            typename F::Stage &qn = q[(il + 1) & 3];
+            F::prepare(qn, hn);
+            const typename F::Scales gs = F::scales(hn, (il + 1) & 3);
+            typename F::Piece pc;
 #pragma unroll
             for (int n = 0; n < 16; ++n) {
                 const int k = n >> 2, tf = n & 3;
                 acc[tf] = mfma32<XT>(acur[k], bq[(16 * il + n) & 7], acc[tf]);
-                const int k2 = n >> 2, piece = n & 3;
-                const bool hi = k2 >= 2;
-                const float sc = hi ? gs.hi : gs.lo;
-                const float dm = hi ? gs.dm_hi : gs.dm_lo;
-                if (piece == 0) {
-                    m0 = nibble_bytes((k2 & 1) ? qn.z : qn.x, hi);
-                    const f32x2 f = nibbles_f32<false>(m0);
-                    o0 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
-                } else if (piece == 1) {
-                    const f32x2 f = nibbles_f32<true>(m0);
-                    o1 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
-                } else if (piece == 2) {
-                    m1 = nibble_bytes((k2 & 1) ? qn.w : qn.y, hi);
-                    const f32x2 f = nibbles_f32<false>(m1);
-                    o2 = pack2<XT>(sc * f[0] - dm, sc * f[1] - dm);
-                } else {
-                    const f32x2 f = nibbles_f32<true>(m1);
-                    anext[k2] = u32x4{o0, o1, o2, pack2<XT>(sc * f[0] - dm, sc * f[1] - dm)};
-                }
+                F::template piece<XT>(n >> 2, n & 3, (il + 1) & 3, qn, hn, gs, pc, anext[n >> 2]);
                 const int nr = n + kLook;
                 bq[(16 * il + nr) & 7] = nr < 16 ? read_b(il, nr) : read_b((il + 1) & 3, nr - 16);
             }
@@ -587,10 +801,14 @@ static int env_or(const char *name, int dflt) {
     return r > 0 ? r : dflt;
 }
 
-template <int XT, int YT>
+template <int T, int XT, int YT>
 static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
                                 int K, hipStream_t st) {
     constexpr int TM = 128;  // tokens per workgroup tile
+    // 32-bit buffer offsets: the x tile, and a wave's 32 rows of Q6_K weights
+    const int64_t row_bytes = (int64_t)(K / 256) * GemmFmt<T>::kBytes;
+    if ((int64_t)TM * K * 2 > 0x7FFFFFFF || (T == 14 && row_bytes * kW8Rows > 0x7FFFFFFF))
+        return hipErrorInvalidValue;
     GemmParams p{};
     p.y = y;
     p.w = w;
@@ -620,24 +838,32 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     }
     p.total_units = tiles * splits;
     p.units_per_xcd = (p.total_units + 7) / 8;
-    gemm_kernel<XT, YT><<<8 * p.units_per_xcd, 512, 0, st>>>(p);
+    gemm_kernel<T, XT, YT><<<8 * p.units_per_xcd, 512, 0, st>>>(p);
     if (splits > 1)  // 16 float4 per thread; at most units_per_xcd / splits + 1 tiles per XCD
         gemm_reduce_kernel<YT><<<8 * 16 * ((p.units_per_xcd + splits - 1) / splits + 1), 512, 0,
                                  st>>>(p);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(void *y, int y_dtype, const uint8_t *w, const void *x, int x_dtype,
-                       int M, int N, int K, hipStream_t st) {
+template <int T>
+static hipError_t launch_gemm_xy(void *y, int y_dtype, const uint8_t *w, const void *x,
+                                 int x_dtype, int M, int N, int K, hipStream_t st) {
     const uint16_t *xx = static_cast<const uint16_t *>(x);
     if (x_dtype == RXQ4_DTYPE_BF16) {
         if (y_dtype == RXQ4_DTYPE_BF16)
-            return launch_gemm_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, N, K, st);
-        return launch_gemm_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
+            return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, N, K, st);
+        return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
     }
     if (y_dtype == RXQ4_DTYPE_F16)
-        return launch_gemm_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, N, K, st);
-    return launch_gemm_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
+        return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, N, K, st);
+    return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
+}
+
+hipError_t launch_gemm(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,
+                       int x_dtype, int M, int N, int K, hipStream_t st) {
+    if (ggml_type == 14) return launch_gemm_xy<14>(y, y_dtype, w, x, x_dtype, M, N, K, st);
+    if (ggml_type == 13) return launch_gemm_xy<13>(y, y_dtype, w, x, x_dtype, M, N, K, st);
+    return launch_gemm_xy<12>(y, y_dtype, w, x, x_dtype, M, N, K, st);
 }
 
 template <int XT, int YT>

@@ -53,11 +53,6 @@ struct KqFormat<14> {
     static constexpr int kBytes = 210;
 };
 
-// v_alignbyte: bytes r.. of the 8-byte value hi:lo.
-__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, int r) {
-    return __builtin_amdgcn_alignbyte(hi, lo, (uint32_t)r);
-}
-
 // 16 bytes at an even byte offset: the aligned 16 bytes at off & ~3 plus the
 // next dword (20 bytes cover the 16 wanted ones).
 struct Raw16 {
@@ -777,36 +772,19 @@ static void launch_kq_tok(dim3 grid, void *y, const uint8_t *w, const uint16_t *
     kq_tokens_kernel<T, XT, YT, RT, TT><<<grid, 256, 0, st>>>(y, w, x, M, N, K);
 }
 
-// Tile: 32 rows when there are enough tiles to fill the chip, 16 x TT tokens
-// with TT up to 8 (one 16-token fragment for small batches).
+// Small batches (the C ABI sends more than 16 tokens to the eight-wave GEMM
+// of gemm_q4k.hip): one 16-token fragment per workgroup (grid.y walks the
+// 16-token chunks), 32 rows when that still gives a workgroup per CU.
 template <int T, int XT, int YT>
 static hipError_t launch_kq_tokens_xy(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
                                       int K, hipStream_t st) {
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-    // The largest tile (most reuse of each dequantised weight and x
-    // fragment) that still gives a workgroup per CU; tiles never exceed
-    // the token count (one workgroup per CU measured best at m = 512).
-    int tt = N <= 16 ? 1 : N <= 32 ? 2 : N <= 64 ? 4 : 8, rt = 2;
-    auto wgs = [&](int r, int t) {
-        return (int64_t)((M + 16 * r - 1) / (16 * r)) * ((N + 16 * t - 1) / (16 * t));
-    };
-    while (wgs(rt, tt) < cus && (rt > 1 || tt > 1)) {
-        if (rt > 1) rt = 1;
-        else tt /= 2;
-    }
-    const dim3 grid((M + 16 * rt - 1) / (16 * rt), (N + 16 * tt - 1) / (16 * tt));
+    const int chunks = (N + 15) / 16;
+    const int rt = (int64_t)((M + 31) / 32) * chunks >= cus ? 2 : 1;
+    const dim3 grid((M + 16 * rt - 1) / (16 * rt), chunks);
     if (grid.y > 65535) return hipErrorInvalidValue;
-    if (rt == 2) {
-        if (tt == 1) launch_kq_tok<T, XT, YT, 2, 1>(grid, y, w, x, M, N, K, st);
-        else if (tt == 2) launch_kq_tok<T, XT, YT, 2, 2>(grid, y, w, x, M, N, K, st);
-        else if (tt == 4) launch_kq_tok<T, XT, YT, 2, 4>(grid, y, w, x, M, N, K, st);
-        else launch_kq_tok<T, XT, YT, 2, 8>(grid, y, w, x, M, N, K, st);
-    } else {
-        if (tt == 1) launch_kq_tok<T, XT, YT, 1, 1>(grid, y, w, x, M, N, K, st);
-        else if (tt == 2) launch_kq_tok<T, XT, YT, 1, 2>(grid, y, w, x, M, N, K, st);
-        else if (tt == 4) launch_kq_tok<T, XT, YT, 1, 4>(grid, y, w, x, M, N, K, st);
-        else launch_kq_tok<T, XT, YT, 1, 8>(grid, y, w, x, M, N, K, st);
-    }
+    if (rt == 2) launch_kq_tok<T, XT, YT, 2, 1>(grid, y, w, x, M, N, K, st);
+    else launch_kq_tok<T, XT, YT, 1, 1>(grid, y, w, x, M, N, K, st);
     return hipGetLastError();
 }
 

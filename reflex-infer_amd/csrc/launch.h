@@ -60,10 +60,11 @@ constexpr int kMaxSmallBatch = 16;
 hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void *x,
                               int x_dtype, int M, int n_tok, int K, hipStream_t stream);
 
-// MFMA GEMM: y[N x M] = x[N x K] . dequant(W)^T with x/weight tiles of the
-// x type (fp16 or bf16) and fp32 accumulation; y fp32/fp16/bf16.
-hipError_t launch_gemm(void *y, int y_dtype, const uint8_t *w, const void *x, int x_dtype,
-                       int M, int N, int K, hipStream_t stream);
+// MFMA GEMM: y[N x M] = x[N x K] . dequant(W)^T for Q4_K (12), Q5_K (13)
+// or Q6_K (14) weights, with x/weight tiles of the x type (fp16 or bf16) and
+// fp32 accumulation; y fp32/fp16/bf16.
+hipError_t launch_gemm(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,
+                       int x_dtype, int M, int N, int K, hipStream_t stream);
 
 // Embedding rows: dst[i, :] = fp16(dequant(W[id_i, :])).  ids == nullptr means
 // the single row token_id (no range check, as in the reference).

@@ -78,6 +78,11 @@ __device__ __forceinline__ void scale_one(uint32_t s0, uint32_t s1, uint32_t s2,
     *mn = (q >> sh) & 0xFFu;
 }
 
+// v_alignbyte: bytes r.. (r < 4) of the 8-byte value hi:lo.
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, int r) {
+    return __builtin_amdgcn_alignbyte(hi, lo, (uint32_t)r);
+}
+
 // Sum over the lanes of aligned groups of `width` lanes (power of two <= 64).
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {

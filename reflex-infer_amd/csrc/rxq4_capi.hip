@@ -200,9 +200,12 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
                            y_dtype == RXQ4_DTYPE_F32 ? rxq4::kEpiF32 : rxq4::kEpiF16, stream);
     }
     hipError_t e;
-    if (kquant_type(ggml_type))
+    if (kquant_type(ggml_type) && N <= rxq4::kMaxSmallBatch)
         e = rxq4::launch_kq_tokens(ggml_type, y, y_dtype, static_cast<const uint8_t *>(w), x,
                                    x_dtype, M, N, K, st);
+    else if (kquant_type(ggml_type))
+        e = rxq4::launch_gemm(ggml_type, y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype,
+                              M, N, K, st);
     else if (N <= rxq4::kMaxRegTokens && x_dtype == RXQ4_DTYPE_F16 && multi_token_gemv())
         // 2..4 fp16 tokens: the decode GEMV with every token's activations in
         // registers (one weight read, the nibble decode shared by the tokens)
@@ -212,7 +215,7 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
         e = rxq4::launch_gemv_tokens(y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M,
                                      N, K, st);
     else
-        e = rxq4::launch_gemm(y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M, N, K,
+        e = rxq4::launch_gemm(12, y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M, N, K,
                               st);
     return from_hip(e, fn);
 }
