@@ -612,7 +612,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         }
         return;
     }
-    const bool vec_ok = (p.M & 3) == 0;
+    // 4 outputs per store need M % 4 == 0 and a 16-byte aligned y (any
+    // y alignment the element size allows is accepted: then element stores)
+    const bool vec_ok = (p.M & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
 #pragma unroll
     for (int tf = 0; tf < NT; ++tf)
 #pragma unroll
@@ -655,7 +657,8 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
     }
     if (tok >= p.N || row >= p.M) return;
     const int valid = min(4, p.M - row);
-    store4<YT>(p.y, (int64_t)tok * p.M + row, sum, (p.M & 3) == 0 && valid == 4, valid);
+    const bool vec_ok = (p.M & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
+    store4<YT>(p.y, (int64_t)tok * p.M + row, sum, vec_ok && valid == 4, valid);
 }
 
 // ---------------------------------------------------------------------------

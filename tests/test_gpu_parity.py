@@ -18,6 +18,7 @@ import torch
 import rxq4
 from oracle import oracle as orc
 from rxq4 import api, capi
+from tests import kquant_blocks as kb
 from tests import util
 
 pytestmark = pytest.mark.gpu
@@ -337,6 +338,27 @@ def test_multi_token_gemv_equals_per_token_gemv(M, N, K):
         capi.gemv_f16(g16, W, x[t], M, K)
         capi.gemv_f32(g32, W, x[t], M, K)
         assert torch.equal(y16[t], g16) and torch.equal(y32[t], g32)
+
+
+@pytest.mark.parametrize("t", [12, 14])
+@pytest.mark.parametrize("K", [512, 2048])  # one K split / four (the reduction kernel stores)
+def test_gemm_output_at_any_element_alignment(t, K):
+    """y one element past a 16-byte boundary: the kernels fall back to
+    element stores and write the same values as into an aligned y."""
+    M, N = 512, 40
+    Wn = (util.weights(160, M, K) if t == 12 else kb.random_blocks(t, util.rng(161), M, K))
+    W = dev(Wn)
+    xb = util.f32_to_bf16_bits(util.gaussian(162, (N, K)))
+    x = torch.from_numpy(xb.view(np.int16)).cuda().view(torch.bfloat16)
+    for dtype in (torch.bfloat16, torch.float32):
+        ya = torch.empty((N, M), dtype=dtype, device="cuda")
+        capi.gemm(ya, W, x, M, N, K, ggml_type=t)
+        buf = torch.full((N * M + 8,), -7.0, dtype=dtype, device="cuda")
+        yo = buf[1:1 + N * M].view(N, M)
+        assert yo.data_ptr() % 16 != 0
+        capi.gemm(yo, W, x, M, N, K, ggml_type=t)
+        assert torch.equal(yo, ya)
+        assert buf[0].item() == -7.0 and bool((buf[1 + N * M:] == -7.0).all())
 
 
 def test_gemm_n1_is_the_gemv():
