@@ -188,3 +188,22 @@ def test_kq_gemm_n1_is_the_gemv():
     y2 = torch.empty(M, dtype=torch.float16, device="cuda")
     capi.gemv_f16(y2, W, x, M, K, ggml_type=14)
     assert torch.equal(y[0], y2)
+
+
+@pytest.mark.parametrize("t", [13, 14])
+def test_kq_gemm_full_size_sampled_rows(t):
+    """m = 512 on [11008 x 2048] and [2048 x 11008] (split K) with ggml-quantised
+    weights: 192 sampled rows against the fp64 oracle on the bf16-rounded
+    weights, fp32 out."""
+    for M, K in ((11008, 2048), (2048, 11008)):
+        print(f"kq gemm full size type {t} M={M} K={K}", flush=True)
+        N = 512
+        g = torch.Generator(device="cuda").manual_seed(770 + t + K)
+        W = capi.quantize_ggml(torch.randn((M, K), generator=g, device="cuda") * 0.02, t)
+        x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+        y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+        capi.gemm(y, W, x, M, N, K, ggml_type=t)
+        rows = np.sort(util.rng(771 + t).choice(M, 192, replace=False))
+        Wn = W[torch.from_numpy(rows).cuda()].cpu().numpy()
+        ref = orc.kq_gemm_f64(Wn, K, t, x.float().cpu().numpy(), "bf16")
+        assert util.rel_err(y.cpu().numpy()[:, rows], ref) <= util.TOL
