@@ -90,7 +90,7 @@ int rxq4_gemv_f32(float *y, const void *w, int ggml_type, const void *x, int M, 
  * for Q4_K, N <= 4 runs the decode GEMV with every token's activations in
  * registers (per token bit-identical to the GEMV), N <= 16 the multi-token
  * MFMA kernel, larger N the MFMA GEMM; Q5_K / Q6_K run their multi-token
- * MFMA kernel up to N = 16 and the same GEMM above. */
+ * MFMA kernel up to N = 16 and the same GEMM above.
  * Replaces kernels::gemm_quant_batched (reference q4_gemm.cu:2023-2029,
  * 1707-1740). */
 int rxq4_gemm_f16(void *y, const void *w, int ggml_type, const void *x, int M, int N,

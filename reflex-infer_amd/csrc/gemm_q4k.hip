@@ -666,19 +666,23 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
 // x 16 tokens.  The K super-blocks are dealt to the waves round-robin (wave
 // w: w, w+KW, ...); each wave computes RT 16x16 fragments with
 // v_mfma_f32_16x16x32 (A = 16 weight rows, B = the 16 tokens), so one x
-// fragment serves RT row tiles.  Lane (row li, group g) loads the 32 qs bytes
-// of quant group g of its row's block with two 16-byte loads and needs only
-// that group's scales; k-step s (0..7) of a super-block gives it nibble
-// s / 4 of bytes 8*(s % 4) .. +7, i.e. elements 64g + 32*(s/4) + 8*(s%4) + e,
-// and the x fragment of the step is read at those elements.  (With one
-// 8-byte load per group and step, the weight stream alone ran 2.7 us slower
-// on gate+up at m = 8.)  Each wave keeps two super-blocks of weights and x
+// fragment serves RT row tiles.  Two weight layouts (WIDE):
+//   * WIDE (up to 8 tokens): lane (row li, group g) loads the 32 qs bytes of
+//     quant group g with two 16-byte loads and needs only that group's
+//     scales; k-step s (0..7) gives it nibble s / 4 of bytes 8*(s % 4) .. +7,
+//     i.e. elements 64g + 32*(s/4) + 8*(s%4) + e, and the x fragment of the
+//     step is read at those elements (four 16-byte pieces per token);
+//   * otherwise lane g loads bytes 8g .. 8g+7 of every quant group (four
+//     8-byte loads) and the x fragments are 64-byte runs per token.
+// On 36 distinct gate+up layers the wide loads took m = 8 from 14.7 to
+// 12.9 us, while m = 16, where all 16 token lanes read x, lost to the
+// scattered x pieces (down 16.2 -> 19.3 us).  Each wave keeps two super-blocks of weights and x
 // in flight (loads unconditional, clamped to the last super-block, so the
 // compiler's vmcnt waits stay exact).  x is read through a buffer resource
 // bounded at N*K elements: the lanes of tokens >= N read past it and get
 // zeros without touching memory.  Partial sums are added in wave order
 // through LDS.
-template <int XT, int YT, int RT, int KW>
+template <int XT, int YT, int RT, int KW, bool WIDE>
 __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
     void *__restrict__ y, const uint8_t *__restrict__ w, const uint16_t *__restrict__ x, int M,
     int N, int K) {
@@ -695,13 +699,18 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
 #pragma unroll
     for (int t = 0; t < RT; ++t) wr[t] = w + min(row0 + 16 * t + li, M - 1) * row_bytes;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, N * K * 2);
-    const int xoff = li * K * 2 + 128 * g;  // bytes; >= N*K*2 for tokens >= N
+    // bytes; >= N*K*2 for tokens >= N
+    const int xoff = li * K * 2 + (WIDE ? 128 * g : 16 * g);
     const int n_w = wave < nb ? (nb - 1 - wave) / KW + 1 : 0;  // super-blocks of this wave
 
+    // x element of k-step s (0..7) for this lane's group g, relative to the
+    // super-block: WIDE 64g + 32*(s/4) + 8*(s%4); otherwise 64*(s/2) +
+    // 32*(s%2) + 8g (quant group s/2, nibble s%2, bytes 8g .. 8g+7).
+    auto x_elem = [](int s) { return WIDE ? 32 * (s >> 2) + 8 * (s & 3) : 64 * (s >> 1) + 32 * (s & 1); };
     struct Sb {
         u32x4 hdr[RT];
-        u32x4 q[RT][2];  // qs bytes 32g .. 32g+31
-        u32x4 b[8];      // x of k-step s: elements 64g + 32*(s/4) + 8*(s%4) + (0..7)
+        u32x4 q[RT][2];  // WIDE: qs bytes 32g .. 32g+31; else bytes 32il + 8g .. +7, il = 0..3
+        u32x4 b[8];
     };
     auto load = [&](int i, Sb &o) {
         const int sb = min(wave + i * KW, nb - 1);
@@ -709,12 +718,20 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
         for (int t = 0; t < RT; ++t) {
             const uint8_t *blk = wr[t] + sb * kBlockBytes;
             o.hdr[t] = load16(blk);
-            o.q[t][0] = load16(blk + 16 + 32 * g);
-            o.q[t][1] = load16(blk + 32 + 32 * g);
+            if (WIDE) {
+                o.q[t][0] = load16(blk + 16 + 32 * g);
+                o.q[t][1] = load16(blk + 32 + 32 * g);
+            } else {
+                u32x2 v[4];
+#pragma unroll
+                for (int il = 0; il < 4; ++il)
+                    v[il] = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * il + 8 * g);
+                o.q[t][0] = u32x4{v[0].x, v[0].y, v[1].x, v[1].y};
+                o.q[t][1] = u32x4{v[2].x, v[2].y, v[3].x, v[3].y};
+            }
         }
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-            o.b[s] = buffer_load16(xr, xoff + 2 * (sb * 256 + 32 * (s >> 2) + 8 * (s & 3)));
+        for (int s = 0; s < 8; ++s) o.b[s] = buffer_load16(xr, xoff + 2 * (sb * 256 + x_elem(s)));
     };
     f32x4 acc[RT];
 #pragma unroll
@@ -722,14 +739,26 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
     auto compute = [&](const Sb &o) {
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const GroupScales gsc = group_scales(o.hdr[t], g);
+            if (WIDE) {
+                const GroupScales gsc = group_scales(o.hdr[t], g);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const u32x4 &w = o.q[t][(s >> 1) & 1];
-                const bool hi = s >= 4;
-                const u32x4 a = dequant8<XT>((s & 1) ? w.z : w.x, (s & 1) ? w.w : w.y, hi,
-                                             hi ? gsc.hi : gsc.lo, hi ? gsc.dm_hi : gsc.dm_lo);
-                acc[t] = mfma<XT>(a, o.b[s], acc[t]);
+                for (int s = 0; s < 8; ++s) {
+                    const u32x4 &w = o.q[t][(s >> 1) & 1];
+                    const bool hi = s >= 4;
+                    const u32x4 a = dequant8<XT>((s & 1) ? w.z : w.x, (s & 1) ? w.w : w.y, hi,
+                                                 hi ? gsc.hi : gsc.lo, hi ? gsc.dm_hi : gsc.dm_lo);
+                    acc[t] = mfma<XT>(a, o.b[s], acc[t]);
+                }
+            } else {
+#pragma unroll
+                for (int il = 0; il < 4; ++il) {
+                    const GroupScales gsc = group_scales(o.hdr[t], il);
+                    const u32x4 &w = o.q[t][il >> 1];
+                    const uint32_t v0 = (il & 1) ? w.z : w.x, v1 = (il & 1) ? w.w : w.y;
+                    acc[t] = mfma<XT>(dequant8<XT>(v0, v1, false, gsc.lo, gsc.dm_lo), o.b[2 * il], acc[t]);
+                    acc[t] = mfma<XT>(dequant8<XT>(v0, v1, true, gsc.hi, gsc.dm_hi), o.b[2 * il + 1],
+                                      acc[t]);
+                }
             }
         }
     };
@@ -878,13 +907,20 @@ static void launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, int M,
     // four waves per CU (1024 waves); a measured sweep of 1/2/4 row tiles and
     // 1/2/4/8 waves on gate+up [22016 x 2048], down [2048 x 11008] and QKV
     // [2560 x 2048] at 2..16 tokens put these two shapes first.
+    // Up to 8 tokens the wide weight loads win (the x lanes of tokens >= N
+    // read nothing); with 9..16 tokens the x fragments' 64-byte runs per
+    // token matter more (measured on 36 distinct layers).
     constexpr int kWaves = 4;
     const int t2 = (M + 31) / 32;
-    if (t2 * kWaves >= 1024)
-        gemv_tokens_kernel<XT, YT, 2, kWaves><<<t2, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
-    else
-        gemv_tokens_kernel<XT, YT, 1, kWaves>
-            <<<(M + 15) / 16, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+    const bool wide = n_tok <= 8;
+    if (t2 * kWaves >= 1024) {
+        if (wide) gemv_tokens_kernel<XT, YT, 2, kWaves, true><<<t2, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+        else gemv_tokens_kernel<XT, YT, 2, kWaves, false><<<t2, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+    } else {
+        const int t1 = (M + 15) / 16;
+        if (wide) gemv_tokens_kernel<XT, YT, 1, kWaves, true><<<t1, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+        else gemv_tokens_kernel<XT, YT, 1, kWaves, false><<<t1, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+    }
 }
 
 hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void *x,
