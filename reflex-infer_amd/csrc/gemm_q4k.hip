@@ -709,7 +709,8 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
     auto x_elem = [](int s) { return WIDE ? 32 * (s >> 2) + 8 * (s & 3) : 64 * (s >> 1) + 32 * (s & 1); };
     struct Sb {
         u32x4 hdr[RT];
-        u32x4 q[RT][2];  // WIDE: qs bytes 32g .. 32g+31; else bytes 32il + 8g .. +7, il = 0..3
+        u32x4 qw[RT][2];  // WIDE: qs bytes 32g .. 32g+31
+        u32x2 q[RT][4];   // otherwise: bytes 32il + 8g .. +7 of quant group il
         u32x4 b[8];
     };
     auto load = [&](int i, Sb &o) {
@@ -719,15 +720,12 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
             const uint8_t *blk = wr[t] + sb * kBlockBytes;
             o.hdr[t] = load16(blk);
             if (WIDE) {
-                o.q[t][0] = load16(blk + 16 + 32 * g);
-                o.q[t][1] = load16(blk + 32 + 32 * g);
+                o.qw[t][0] = load16(blk + 16 + 32 * g);
+                o.qw[t][1] = load16(blk + 32 + 32 * g);
             } else {
-                u32x2 v[4];
 #pragma unroll
                 for (int il = 0; il < 4; ++il)
-                    v[il] = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * il + 8 * g);
-                o.q[t][0] = u32x4{v[0].x, v[0].y, v[1].x, v[1].y};
-                o.q[t][1] = u32x4{v[2].x, v[2].y, v[3].x, v[3].y};
+                    o.q[t][il] = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * il + 8 * g);
             }
         }
 #pragma unroll
@@ -743,7 +741,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
                 const GroupScales gsc = group_scales(o.hdr[t], g);
 #pragma unroll
                 for (int s = 0; s < 8; ++s) {
-                    const u32x4 &w = o.q[t][(s >> 1) & 1];
+                    const u32x4 &w = o.qw[t][(s >> 1) & 1];
                     const bool hi = s >= 4;
                     const u32x4 a = dequant8<XT>((s & 1) ? w.z : w.x, (s & 1) ? w.w : w.y, hi,
                                                  hi ? gsc.hi : gsc.lo, hi ? gsc.dm_hi : gsc.dm_lo);
@@ -753,11 +751,12 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
 #pragma unroll
                 for (int il = 0; il < 4; ++il) {
                     const GroupScales gsc = group_scales(o.hdr[t], il);
-                    const u32x4 &w = o.q[t][il >> 1];
-                    const uint32_t v0 = (il & 1) ? w.z : w.x, v1 = (il & 1) ? w.w : w.y;
-                    acc[t] = mfma<XT>(dequant8<XT>(v0, v1, false, gsc.lo, gsc.dm_lo), o.b[2 * il], acc[t]);
-                    acc[t] = mfma<XT>(dequant8<XT>(v0, v1, true, gsc.hi, gsc.dm_hi), o.b[2 * il + 1],
-                                      acc[t]);
+                    const u32x4 a_lo =
+                        dequant8<XT>(o.q[t][il].x, o.q[t][il].y, false, gsc.lo, gsc.dm_lo);
+                    const u32x4 a_hi =
+                        dequant8<XT>(o.q[t][il].x, o.q[t][il].y, true, gsc.hi, gsc.dm_hi);
+                    acc[t] = mfma<XT>(a_lo, o.b[2 * il], acc[t]);
+                    acc[t] = mfma<XT>(a_hi, o.b[2 * il + 1], acc[t]);
                 }
             }
         }
