@@ -685,7 +685,7 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
 template <int XT, int YT, int RT, int KW, bool WIDE>
 __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
     void *__restrict__ y, const uint8_t *__restrict__ w, const uint16_t *__restrict__ x, int M,
-    int N, int K) {
+    int N, int K, float *__restrict__ ws, int sb_per_split) {
     __shared__ f32x4 part[KW][RT][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -701,7 +701,11 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, N * K * 2);
     // bytes; >= N*K*2 for tokens >= N
     const int xoff = li * K * 2 + (WIDE ? 128 * g : 16 * g);
-    const int n_w = wave < nb ? (nb - 1 - wave) / KW + 1 : 0;  // super-blocks of this wave
+    // Super-blocks [sb_lo, sb_hi) of K split blockIdx.y (all of K without a
+    // split), dealt to the waves round-robin.
+    const int sb_lo = blockIdx.y * sb_per_split, sb_hi = min(nb, sb_lo + sb_per_split);
+    const int n_sb = sb_hi - sb_lo;
+    const int n_w = wave < n_sb ? (n_sb - 1 - wave) / KW + 1 : 0;  // super-blocks of this wave
 
     // x element of k-step s (0..7) for this lane's group g, relative to the
     // super-block: WIDE 64g + 32*(s/4) + 8*(s%4); otherwise 64*(s/2) +
@@ -714,7 +718,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
         u32x4 b[8];
     };
     auto load = [&](int i, Sb &o) {
-        const int sb = min(wave + i * KW, nb - 1);
+        const int sb = min(sb_lo + wave + i * KW, sb_hi - 1);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
             const uint8_t *blk = wr[t] + sb * kBlockBytes;
@@ -788,10 +792,27 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = row0 + 16 * t + 4 * g + r;
-                if (row < M) store_out<YT>(y, (int64_t)li * M + row, sum[r]);
+                if (row >= M) continue;
+                if (ws)  // split K: fp32 partial [split][token][row]
+                    ws[((int64_t)blockIdx.y * N + li) * M + row] = sum[r];
+                else
+                    store_out<YT>(y, (int64_t)li * M + row, sum[r]);
             }
         }
     }
+}
+
+// y[i] = sum over the K splits, in split order, of the partials ws[split][i]
+// (i over N x M, token-major).
+template <int YT>
+__global__ __launch_bounds__(256) void tokens_reduce_kernel(void *__restrict__ y,
+                                                            const float *__restrict__ ws,
+                                                            int64_t n, int splits) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float s = ws[i];
+    for (int k = 1; k < splits; ++k) s += ws[(int64_t)k * n + i];
+    store_out<YT>(y, i, s);
 }
 
 // Split-K workspace: one allocation per device on first use, grown on demand
@@ -899,27 +920,56 @@ hipError_t launch_gemm(int ggml_type, void *y, int y_dtype, const uint8_t *w, co
 }
 
 template <int XT, int YT>
-static void launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, int M, int n_tok,
-                            int K, hipStream_t st) {
+static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, int M, int n_tok,
+                                  int K, hipStream_t st) {
     // Four waves split K.  Two row tiles per wave halve the x traffic per
     // weight byte and pay off once there are enough of them to give about
     // four waves per CU (1024 waves); a measured sweep of 1/2/4 row tiles and
     // 1/2/4/8 waves on gate+up [22016 x 2048], down [2048 x 11008] and QKV
-    // [2560 x 2048] at 2..16 tokens put these two shapes first.
+    // [2560 x 2048] at 2..16 tokens put these two shapes first.  Long rows
+    // with few row tiles (down) also split K over workgroups: 32-row tiles x
+    // up to CUs / tiles splits of at least 8 super-blocks, fp32 partials
+    // summed in split order by tokens_reduce_kernel (down m = 8: 12.4 us
+    // unsplit on 128 workgroups).
     // Up to 8 tokens the wide weight loads win (the x lanes of tokens >= N
     // read nothing); with 9..16 tokens the x fragments' 64-byte runs per
     // token matter more (measured on 36 distinct layers).
     constexpr int kWaves = 4;
+    const int nb = K / 256;
     const int t2 = (M + 31) / 32;
     const bool wide = n_tok <= 8;
-    if (t2 * kWaves >= 1024) {
-        if (wide) gemv_tokens_kernel<XT, YT, 2, kWaves, true><<<t2, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
-        else gemv_tokens_kernel<XT, YT, 2, kWaves, false><<<t2, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+    const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+    int splits = 1;
+    if (t2 * kWaves < 1024 && nb >= 16) splits = std::max(1, std::min(cus / t2, nb / 8));
+    if (t2 * kWaves >= 1024 || splits > 1) {
+        const int sbps = (nb + splits - 1) / splits;
+        splits = (nb + sbps - 1) / sbps;
+        float *ws = nullptr;
+        if (splits > 1) {
+            hipError_t e = device_workspace((size_t)splits * n_tok * M * sizeof(float), &ws);
+            if (e != hipSuccess) return e;
+        }
+        const dim3 grid(t2, splits);
+        if (wide)
+            gemv_tokens_kernel<XT, YT, 2, kWaves, true>
+                <<<grid, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, ws, sbps);
+        else
+            gemv_tokens_kernel<XT, YT, 2, kWaves, false>
+                <<<grid, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, ws, sbps);
+        if (splits > 1) {
+            const int64_t n = (int64_t)n_tok * M;
+            tokens_reduce_kernel<YT><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(y, ws, n, splits);
+        }
     } else {
         const int t1 = (M + 15) / 16;
-        if (wide) gemv_tokens_kernel<XT, YT, 1, kWaves, true><<<t1, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
-        else gemv_tokens_kernel<XT, YT, 1, kWaves, false><<<t1, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K);
+        if (wide)
+            gemv_tokens_kernel<XT, YT, 1, kWaves, true>
+                <<<t1, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
+        else
+            gemv_tokens_kernel<XT, YT, 1, kWaves, false>
+                <<<t1, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
     }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void *x,
@@ -927,16 +977,12 @@ hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void
     const uint16_t *xx = static_cast<const uint16_t *>(x);
     if (x_dtype == RXQ4_DTYPE_BF16) {
         if (y_dtype == RXQ4_DTYPE_BF16)
-            launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, n_tok, K, st);
-        else
-            launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
-    } else {
-        if (y_dtype == RXQ4_DTYPE_F16)
-            launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, n_tok, K, st);
-        else
-            launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
+            return launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, n_tok, K, st);
+        return launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
     }
-    return hipGetLastError();
+    if (y_dtype == RXQ4_DTYPE_F16)
+        return launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, n_tok, K, st);
+    return launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
 }
 
 }  // namespace rxq4

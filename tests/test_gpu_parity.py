@@ -273,9 +273,12 @@ def test_lm_head_full_size_properties():
 # partial last tile (8200 = 256 * 32 + 8).
 # (1000, 200) and (264, 130): 16-bit outputs staged through LDS with a
 # partial last row tile and token tile.
+# (2048, 8 / 16, 11008) and (600, 6, 4096): small batches of long rows, K split
+# over workgroups with fp32 partials.
 GEMM_CASES = [(300, 2, 2048), (2048, 5, 2048), (1000, 16, 2048), (2048, 17, 2048),
               (300, 100, 11008), (2048, 512, 2048), (129, 33, 512), (8200, 3, 512),
-              (8200, 16, 256), (1000, 200, 2048), (264, 130, 512)]
+              (8200, 16, 256), (1000, 200, 2048), (264, 130, 512), (2048, 8, 11008),
+              (2048, 16, 11008), (600, 6, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_CASES)
