@@ -389,3 +389,31 @@ def test_gemm_full_size_sampled_rows():
     xv = x.float().cpu().numpy()
     ref = orc.gemm_f64(Wn, K, xv, "bf16")
     assert util.rel_err(y.cpu().numpy()[:, rows], ref) <= util.TOL
+
+
+def test_split_k_paths_replay_in_a_graph():
+    """The split-K GEMM (workspace + reduction launch) and the split
+    small-batch kernel captured in a HIP graph: every replay, with eager
+    work and synchronisation in between, equals the eager result."""
+    cases = [(2048, 512, 11008, torch.bfloat16), (2048, 16, 11008, torch.float16)]
+    for M, N, K, dt in cases:
+        print(f"graph replay M={M} N={N} K={K}", flush=True)
+        g = torch.Generator(device="cuda").manual_seed(180 + N)
+        W = capi.quantize(torch.randn((M, K), generator=g, device="cuda") * 0.02)
+        x = torch.randn((N, K), generator=g, device="cuda").to(dt)
+        y_eager = torch.empty((N, M), dtype=dt, device="cuda")
+        capi.gemm(y_eager, W, x, M, N, K)  # also sizes the workspace before capture
+        torch.cuda.synchronize()
+        y = torch.empty_like(y_eager)
+        s = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            capi.gemm(y, W, x, M, N, K, stream=s)
+        for rep in range(3):
+            y.fill_(0)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, y_eager), f"replay {rep}"
+            # eager work on the same workspace between replays
+            capi.gemm(y_eager, W, x, M, N, K)
+            torch.cuda.synchronize()
