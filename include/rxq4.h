@@ -22,9 +22,11 @@
  *   - `stream` is a hipStream_t (NULL = null stream).  Calls only enqueue
  *     work and nothing synchronises.  Nothing allocates device memory except
  *     the GEMM entry points when they split K over workgroups (few output
- *     tiles, e.g. M = 2048 at N <= 2048): they keep one fp32 partial-sum
- *     workspace per device, allocated on first use and grown when a larger
- *     one is needed (tiles * splits * 128 KiB), and held until exit.
+ *     tiles, e.g. M = 2048 at N <= 2048, or N <= 16 tokens on rows of 16 or
+ *     more super-blocks): they keep one fp32 partial-sum workspace per
+ *     device, allocated on first use and grown when a larger one is needed
+ *     (tiles * splits * 128 KiB, resp. splits * N * M * 4 bytes), and held
+ *     until exit.
  *   - The return value is a reflex::infer::Status value (RXQ4_STATUS_*).
  *     On an error nothing is launched; rxq4_last_error() says why.
  */
