@@ -1,6 +1,8 @@
 // kquant.hip -- Q5_K (ggml type 13) and Q6_K (type 14) weights on gfx950:
 // decode GEMV (fp16 / fp32 / residual-add outputs), Q6_K embedding rows and
-// the multi-token GEMM.  Replaces the reference's Q5_K/Q6_K kernels
+// the small-batch (2..16 token) product; more tokens run the MFMA GEMM of
+// gemm_q4k.hip with the Q5_K / Q6_K format policies.  Replaces the
+// reference's Q5_K/Q6_K kernels
 // (q4_gemm.cu:325-405 dot_q5k_row / dot_q6k_row, 473-489 and 527-543 the
 // GEMVs, 574-616 the Q6_K embedding, 1358-1480 the batched kernels).
 //
@@ -628,9 +630,9 @@ hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, 
 }
 
 // ---------------------------------------------------------------- GEMM
-// Multi-token product y[N x M] = x[N x K] . dequant(W)^T for Q5_K/Q6_K:
-// a workgroup of 4 waves owns 16 weight rows x 16 tokens (grid.y walks the
-// token chunks); the blocks of K are dealt to the waves round-robin and the
+// Small-batch product y[N x M] = x[N x K] . dequant(W)^T for Q5_K/Q6_K:
+// a workgroup of 4 waves owns 16*RT weight rows x 16 tokens (grid.y walks
+// the token chunks); the blocks of K are dealt to the waves round-robin and the
 // partial tiles added in wave order through LDS.  Per 32-k step a lane
 // dequantises the 8 weights of its MFMA src0 fragment (row l%16, k 8*(l/16)..)
 // in fp32 -- Q6_K d*sc*(q-32) exact, Q5_K (d*sc)*q - dmin*m with one
