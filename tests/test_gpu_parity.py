@@ -274,11 +274,13 @@ def test_lm_head_full_size_properties():
 # (1000, 200) and (264, 130): 16-bit outputs staged through LDS with a
 # partial last row tile and token tile.
 # (2048, 8 / 16, 11008) and (600, 6, 4096): small batches of long rows, K split
-# over workgroups with fp32 partials.
+# over workgroups with fp32 partials.  (16400, 7, 512) and (16384, 16, 256):
+# small batches on 64-row workgroups with x staged in LDS (at least one per
+# CU), the first with a partial last tile.
 GEMM_CASES = [(300, 2, 2048), (2048, 5, 2048), (1000, 16, 2048), (2048, 17, 2048),
               (300, 100, 11008), (2048, 512, 2048), (129, 33, 512), (8200, 3, 512),
               (8200, 16, 256), (1000, 200, 2048), (264, 130, 512), (2048, 8, 11008),
-              (2048, 16, 11008), (600, 6, 4096)]
+              (2048, 16, 11008), (600, 6, 4096), (16400, 7, 512), (16384, 16, 256)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_CASES)
@@ -299,7 +301,7 @@ def test_gemm_bf16(M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 3, 2048), (2048, 16, 2048), (1000, 40, 2048),
-                                   (256, 512, 2048), (200, 20, 11008)])
+                                   (256, 512, 2048), (200, 20, 11008), (16400, 9, 256)])
 def test_api_gemm_quant_batched_f16(M, N, K):
     Wn = util.weights(110 + N, M, K)
     x16 = util.x_f16(111 + N, (N, K))
