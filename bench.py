@@ -20,7 +20,8 @@ stream and timed with HIP events recorded on that stream around replays:
                (FETCH_SIZE + WRITE_SIZE scaled by a copy of known size)
   per_kernel   every decode projection, the LM head [151936 x 2048] fp32
                GEMV, the 4096-id Zipf(1.1) embedding gather, and the prefill
-               GEMM at m=512 (TFLOP/s, BASELINE metric's second half)
+               GEMM at m=512 (TFLOP/s, BASELINE metric's second half) and
+               m=2048
   attn_*       decode attention over 4096 and 16384 positions and causal
                prefill of 512 tokens (32 query / 8 KV heads, head_dim 128,
                fp16 KV)
@@ -438,18 +439,21 @@ def main() -> int:
                                                  "GFLOPs": round(2 * m * M * K / med / 1e3, 1)}
         extras["small_batch_decode"] = small
 
-        # Prefill GEMM at m = 512 (bf16 activations, bf16 out).
+        # Prefill GEMM at m = 512 and 2048 (bf16
+        # activations, bf16 out).
         for (M, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):
             ws = [qweights(30_000 + M + i, M, K) for i in range(4)]
-            xb = gen(40_000 + K, (512, K), 1.0).to(torch.bfloat16)
-            yb = torch.empty((512, M), dtype=torch.bfloat16, device=dev)
+            for m in (512, 2048):
+                xb = gen(40_000 + K + m, (m, K), 1.0).to(torch.bfloat16)
+                yb = torch.empty((m, M), dtype=torch.bfloat16, device=dev)
 
-            def gm_launch(i):
-                capi.gemm(yb, ws[i % 4], xb, M, 512, K, stream=sp)
-            med, _ = per_launch(gm_launch, 20)
-            tf = 2 * 512 * M * K / med / 1e6
-            kernels[f"gemm_bf16_m512_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1),
-                                                  "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                def gm_launch(i, xb=xb, yb=yb, m=m):
+                    capi.gemm(yb, ws[i % 4], xb, M, m, K, stream=sp)
+                med, _ = per_launch(gm_launch, 20 if m == 512 else 8)
+                tf = 2 * m * M * K / med / 1e6
+                kernels[f"gemm_bf16_m{m}_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1),
+                                                      "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                del xb, yb
             del ws
         extras["gemm_m512_tflops"] = min(v["TFLOPs"] for k, v in kernels.items()
                                          if k.startswith("gemm_bf16_m512"))
