@@ -804,9 +804,9 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
 
 // Small batch with x staged in LDS, for matrices with at least one 64-row
 // workgroup per CU (gate+up): the 4 waves split rows (16*RT each, all of K)
-// and share each super-block's x tile
-// (16 tokens x 512 bytes), copied once per workgroup by direct-to-LDS loads
-// into a ring of 3 buffers, 2 super-blocks ahead.  Chunk c (16 bytes) of
+// and share each super-block's x tile (16 tokens x 512 bytes), copied once
+// per workgroup by direct-to-LDS loads into a ring of 3 buffers, 2
+// super-blocks ahead.  Chunk c (16 bytes) of
 // token t sits at c ^ (t & 15), so a 16-lane fragment read covers the 64
 // banks once.  Weights use the 16-byte (WIDE) layout of gemv_tokens_kernel.
 // Against gemv_tokens_kernel (x fragments from L2 per wave) on 36 distinct
