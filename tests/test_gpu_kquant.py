@@ -152,7 +152,7 @@ def test_q6k_embedding_bit_exact(K):
 # K = 11008 and 2304 give Q6_K rows that start on odd 2-byte boundaries)
 @pytest.mark.parametrize("M,N,K", [(300, 2, 2048), (129, 17, 512), (64, 40, 11008), (33, 5, 256),
                                    (600, 130, 1024), (2100, 70, 512), (1000, 300, 2304),
-                                   (96, 40, 256)])
+                                   (96, 40, 256), (40, 24, 65536)])
 def test_kq_gemm(t, M, N, K):
     print(f"kq gemm type {t} M={M} N={N} K={K}", flush=True)
     Wn = kb.random_blocks(t, util.rng(740 + t + N), M, K)

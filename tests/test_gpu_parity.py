@@ -277,12 +277,13 @@ def test_lm_head_full_size_properties():
 # over workgroups with fp32 partials.  (16400, 7, 512) and (16384, 16, 256):
 # small batches on 64-row workgroups with x staged in LDS (at least one per
 # CU), the first with a partial last tile.  (520, 129, 256): one super-block
-# per row and a last token tile of one token.
+# per row and a last token tile of one token.  (300, 20, 65536): the largest
+# K, 128 K-splits.
 GEMM_CASES = [(300, 2, 2048), (2048, 5, 2048), (1000, 16, 2048), (2048, 17, 2048),
               (300, 100, 11008), (2048, 512, 2048), (129, 33, 512), (8200, 3, 512),
               (8200, 16, 256), (1000, 200, 2048), (264, 130, 512), (2048, 8, 11008),
               (2048, 16, 11008), (600, 6, 4096), (16400, 7, 512), (16384, 16, 256),
-              (520, 129, 256)]
+              (520, 129, 256), (300, 20, 65536)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_CASES)
