@@ -208,3 +208,36 @@ def test_kq_gemm_full_size_sampled_rows(t):
         Wn = W[torch.from_numpy(rows).cuda()].cpu().numpy()
         ref = orc.kq_gemm_f64(Wn, K, t, x.float().cpu().numpy(), "bf16")
         assert util.rel_err(y.cpu().numpy()[:, rows], ref) <= util.TOL
+
+
+def test_gemm_random_shapes_all_paths():
+    """Seeded random shapes over every product path (multi-token GEMV,
+    small-batch MFMA with and without the K split or LDS staging, the GEMM
+    with and without split K), all three formats and both x types, against
+    the fp64 oracle on the operand-rounded weights."""
+    r = util.rng(790)
+    for case in range(24):
+        t = int(r.choice([12, 13, 14]))
+        K = 256 * int(r.choice([1, 2, 3, 5, 8, 16, 17, 43]))
+        M = int(r.integers(1, 700))
+        N = int(r.choice([2, 3, 4, 5, 9, 16, 17, 40, 129, 300]))
+        xt = r.choice(["f16", "bf16"])
+        print(f"random gemm case {case}: type {t} M={M} N={N} K={K} x={xt}", flush=True)
+        Wn = util.weights(800 + case, M, K) if t == 12 else kb.random_blocks(t, util.rng(800 + case), M, K)
+        W = dev(Wn)
+        xf = util.gaussian(900 + case, (N, K))
+        y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+        if xt == "bf16":
+            xb = util.f32_to_bf16_bits(xf)
+            x = torch.from_numpy(xb.view(np.int16)).cuda().view(torch.bfloat16)
+            xv = orc.bits_bf16_to_f32(xb)
+        else:
+            x16 = util.x_f16(900 + case, (N, K))
+            x = dev(x16).view(torch.float16)
+            xv = f16(x16)
+        capi.gemm(y, W, x, M, N, K, ggml_type=t)
+        # Q4_K with up to 4 fp16 tokens runs the GEMV (weights unrounded),
+        # everything else the MFMA kernels on weights rounded to the x type
+        wkind = None if (t == 12 and xt == "f16" and N <= 4) else xt
+        ref = orc.kq_gemm_f64(Wn, K, t, xv, wkind)
+        assert util.rel_err(y.cpu().numpy(), ref) <= util.TOL, f"case {case}"
