@@ -286,8 +286,10 @@ struct Slot {
     }
 };
 
+// res: the row's residual (fp16 bits, kEpiAdd), fetched with the row's
+// weights so that the store waits for no further load.
 template <int EPI>
-__device__ __forceinline__ void kq_store(const KqGemvParams &p, int row, float v) {
+__device__ __forceinline__ void kq_store(const KqGemvParams &p, int row, float v, uint32_t res) {
     if (EPI == kEpiF32) {
         static_cast<float *>(p.y)[row] = v;
     } else if (EPI == kEpiF16) {
@@ -295,18 +297,30 @@ __device__ __forceinline__ void kq_store(const KqGemvParams &p, int row, float v
     } else {
         // q4_gemm.cu:774-777: round the projection, add the residual, round.
         const float projected = f16_bits_to_f32(f32_to_f16_bits(v));
-        static_cast<uint16_t *>(p.y)[row] = f32_to_f16_bits(projected + f16_bits_to_f32(p.res[row]));
+        static_cast<uint16_t *>(p.y)[row] = f32_to_f16_bits(projected + f16_bits_to_f32(res));
     }
 }
 
-template <int T, int EPI>
+// Residual of `row` (clamped to the matrix) for kEpiAdd, else 0.
+template <int EPI>
+__device__ __forceinline__ uint32_t kq_res(const KqGemvParams &p, int row) {
+    return EPI == kEpiAdd ? p.res[min(row, p.M - 1)] : 0u;
+}
+
+// PACKED: rows of at most 64 slots packed into wave steps (p.rows_per > 0);
+// else one row per wave.  Two instances, so that each path gets its own
+// register allocation.
+template <int T, int EPI, bool PACKED>
 __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
     constexpr int BYTES = KqFormat<T>::kBytes;
     extern __shared__ u32x4 kq_smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    // Stage x (fp16) and the fp32 sums of its 16-element runs.
-    {
+    const int n_waves = gridDim.x * 4;
+    const int wave_g = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
+    const XLds xl{kq_smem, reinterpret_cast<const float *>(kq_smem + (p.K >> 3))};
+    auto stage_x = [&]() {
+        // x (fp16) and the fp32 sums of its 16-element runs.
         u32x4 *xs = kq_smem;
         float *sums = reinterpret_cast<float *>(kq_smem + (p.K >> 3));
         const u32x4 *xg = reinterpret_cast<const u32x4 *>(p.x);
@@ -323,41 +337,64 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
             }
             sums[r] = s;
         }
-    }
-    __syncthreads();
-    const XLds xl{kq_smem, reinterpret_cast<const float *>(kq_smem + (p.K >> 3))};
-    const int n_waves = gridDim.x * 4;
-    const int wave_g = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (p.rows_per > 0) {
-        // slots = 64 / rows_per lanes per row.
+        __syncthreads();
+    };
+    if constexpr (PACKED) {
+        // slots = 64 / rows_per lanes per row; the wave takes the steps
+        // wave_g + k * n_waves.  Two steps are in flight at all times: step
+        // k + 2 is issued as soon as step k has been computed.  Steps past
+        // the last reload the last one (L2 hits, nothing stored), so every
+        // load is unconditional and the compiler's vmcnt waits count exactly.
         const int sub = lane / p.slots;
         const int slot = lane - sub * p.slots;
         const int b = slot >> 2, u = slot & 3;
-        for (int st = wave_g; st < p.n_units; st += 2 * n_waves) {
-            const int st2 = min(st + n_waves, p.n_units - 1);
-            const int r0a = st * p.rows_per, r0b = st2 * p.rows_per;
-            const int na = min(p.rows_per, p.M - r0a), nb2 = min(p.rows_per, p.M - r0b);
-            const RowRes ra = row_rsrc(p.w + (int64_t)r0a * p.row_bytes, na * p.row_bytes);
-            const RowRes rb = row_rsrc(p.w + (int64_t)r0b * p.row_bytes, nb2 * p.row_bytes);
-            const int boff = sub * p.row_bytes + b * BYTES;
-            Slot<T> A, B;
-            A.load(ra.rs, ra.ex + boff, u);
-            B.load(rb.rs, rb.ex + boff, u);
-            float va = A.dot(ra.ex + boff, u, b * 256, xl);
-            for (int o = p.slots >> 1; o > 0; o >>= 1) va += __shfl_xor(va, o, 64);
-            if (slot == 0 && sub < na) kq_store<EPI>(p, r0a + sub, va);
-            float vb = B.dot(rb.ex + boff, u, b * 256, xl);
-            for (int o = p.slots >> 1; o > 0; o >>= 1) vb += __shfl_xor(vb, o, 64);
-            if (slot == 0 && sub < nb2 && st + n_waves < p.n_units) kq_store<EPI>(p, r0b + sub, vb);
+        const int boff = sub * p.row_bytes + b * BYTES;
+        struct Step {
+            Slot<T> s;
+            RowRes r;
+            int r0, n;
+            uint32_t res;
+        };
+        auto load = [&](int st, Step &o) {
+            const int sc = min(st, p.n_units - 1);
+            o.r0 = sc * p.rows_per;
+            const int rows = min(p.rows_per, p.M - o.r0);
+            o.n = st < p.n_units ? rows : 0;
+            o.r = row_rsrc(p.w + (int64_t)o.r0 * p.row_bytes, rows * p.row_bytes);
+            o.s.load(o.r.rs, o.r.ex + boff, u);
+            o.res = kq_res<EPI>(p, o.r0 + sub);
+        };
+        auto finish = [&](const Step &o) {
+            float v = o.s.dot(o.r.ex + boff, u, b * 256, xl);
+            for (int q = p.slots >> 1; q > 0; q >>= 1) v += __shfl_xor(v, q, 64);
+            if (slot == 0 && sub < o.n) kq_store<EPI>(p, o.r0 + sub, v, o.res);
+        };
+        stage_x();
+        if (wave_g < p.n_units) {
+            Step A, B;
+            int st = wave_g;
+            load(st, A);
+            load(st + n_waves, B);
+            for (; st + 2 * n_waves < p.n_units; st += 2 * n_waves) {
+                finish(A);
+                load(st + 2 * n_waves, A);
+                finish(B);
+                load(st + 3 * n_waves, B);
+            }
+            finish(A);
+            finish(B);
         }
     } else {
+        // One row per wave, its slots 64 at a time, two rounds per load batch
+        // (slots past the row read zeros, d = 0; their x reads are clamped
+        // to the last block).
         const int n_iter = (p.slots + 63) >> 6;
+        stage_x();
         for (int row = wave_g; row < p.M; row += n_waves) {
             const RowRes rr = row_rsrc(p.w + (int64_t)row * p.row_bytes, p.row_bytes);
+            const uint32_t res = kq_res<EPI>(p, row);
             float v = 0.0f;
             for (int c = 0; c < n_iter; c += 2) {
-                // Slots past the row read zeros (d = dmin = 0); their x reads
-                // are clamped to the last block.
                 const int s0 = 64 * c + lane, s1 = s0 + 64;
                 const int b0 = s0 >> 2, b1 = s1 >> 2;
                 const int o0 = rr.ex + b0 * BYTES, o1 = rr.ex + b1 * BYTES;
@@ -369,7 +406,7 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
             }
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-            if (lane == 0) kq_store<EPI>(p, row, v);
+            if (lane == 0) kq_store<EPI>(p, row, v, res);
         }
     }
 }
@@ -465,8 +502,8 @@ __global__ __launch_bounds__(256) void kq_multi_kernel(KqMultiParams p) {
     }
 }
 
-template <int T, int EPI>
-static hipError_t launch_kq_gemv_t(const KqGemvParams &p, hipStream_t st) {
+template <int T, int EPI, bool PACKED>
+static hipError_t launch_kq_gemv_p(const KqGemvParams &p, hipStream_t st) {
     const size_t lds = (size_t)p.K * 2 + (size_t)(p.K / 16) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
@@ -474,13 +511,19 @@ static hipError_t launch_kq_gemv_t(const KqGemvParams &p, hipStream_t st) {
     const int want = (p.n_units + 3) / 4;
     const int grid = std::max(1, std::min(want, cus * wg_per_cu));
     if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_gemv_kernel<T, EPI>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&kq_gemv_kernel<T, EPI, PACKED>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)lds);
         if (e != hipSuccess) return e;
     }
-    kq_gemv_kernel<T, EPI><<<grid, 256, lds, st>>>(p);
+    kq_gemv_kernel<T, EPI, PACKED><<<grid, 256, lds, st>>>(p);
     return hipGetLastError();
+}
+
+template <int T, int EPI>
+static hipError_t launch_kq_gemv_t(const KqGemvParams &p, hipStream_t st) {
+    return p.rows_per > 0 ? launch_kq_gemv_p<T, EPI, true>(p, st)
+                          : launch_kq_gemv_p<T, EPI, false>(p, st);
 }
 
 hipError_t launch_kq_gemv(int ggml_type, const GemvRange &r, const uint16_t *x, int K,

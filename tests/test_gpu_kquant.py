@@ -39,7 +39,10 @@ def f16(bits: np.ndarray) -> np.ndarray:
 # (rows, K): packed rows per wave step (K 2048 -> 2 rows, 256 -> 16 rows,
 # 4096 -> 1 row), long rows (11008: 172 slots, 1536: 24 slots), a partial last
 # step (37 rows), and a K whose x staging needs more than 64 KiB of LDS.
-GEMV_SHAPES = [(256, 2048), (300, 256), (37, 4096), (100, 11008), (64, 1536), (3, 32768)]
+# 70001 x 2048 gives each of the 4096 waves 8-9 packed steps (the pipelined
+# steady state, an odd last step and a reload past the end).
+GEMV_SHAPES = [(256, 2048), (300, 256), (37, 4096), (100, 11008), (64, 1536), (3, 32768),
+               (70001, 2048)]
 
 
 @pytest.mark.parametrize("t", [13, 14])
@@ -60,8 +63,9 @@ def test_kq_gemv_f32_f16(t, M, K):
 
 
 @pytest.mark.parametrize("t", [13, 14])
-def test_kq_gemv_add_in_place(t):
-    M, K = 512, 2048
+@pytest.mark.parametrize("M,K", [(512, 2048), (70001, 2048), (300, 11008)])
+def test_kq_gemv_add_in_place(t, M, K):
+    print(f"kq gemv add in place type {t} M={M} K={K}", flush=True)
     Wn = kb.random_blocks(t, util.rng(710 + t), M, K)
     x16, res16 = util.x_f16(711, K), util.x_f16(712, M)
     y32 = orc.kq_gemv_f32(Wn, K, t, x16)
