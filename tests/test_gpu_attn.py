@@ -40,10 +40,13 @@ def check(got_bits, ref64, ref32):
 
 # (n_heads, n_kv, head_dim, seq_len): GQA 4 (Qwen3-4B-like), MHA, one KV head
 # for 16 query heads (two head groups per KV head), head_dim 64/80/256,
-# empty / one / tile-boundary / multi-chunk sequences.
+# empty / one / tile-boundary / multi-chunk sequences; 7000, 8192 and 16384
+# positions split into 55 and 64 chunks of several tiles each (the combine's
+# maximum of 64).
 DECODE = [(32, 8, 128, 0), (32, 8, 128, 1), (32, 8, 128, 256), (32, 8, 128, 257),
           (32, 8, 128, 1500), (32, 8, 128, 4097), (8, 8, 64, 700), (16, 1, 128, 3000),
-          (4, 2, 80, 333), (4, 1, 256, 2100)]
+          (4, 2, 80, 333), (4, 1, 256, 2100), (16, 1, 128, 7000), (32, 8, 128, 8192),
+          (32, 8, 128, 16384)]
 
 
 @pytest.mark.parametrize("H,KV,D,S", DECODE)
@@ -65,8 +68,10 @@ def test_decode_fp16(H, KV, D, S):
 
 
 @pytest.mark.parametrize("scales", [True, False])
-def test_decode_int8(scales):
-    H, KV, D, S = 32, 8, 128, 2000
+@pytest.mark.parametrize("S", [2000, 9000])
+def test_decode_int8(scales, S):
+    print(f"attention decode int8 S={S} scales={scales}", flush=True)
+    H, KV, D = 32, 8, 128
     r = util.rng(910)
     q = f16(r.standard_normal(H * D))
     ki = r.integers(-127, 128, (S, KV, D)).astype(np.int8)
