@@ -20,13 +20,14 @@
  *   - fp16/bf16 buffers are raw 16-bit patterns; x must be 16-byte aligned.
  *   - K must be a positive multiple of 256 and at most RXQ4_MAX_K.
  *   - `stream` is a hipStream_t (NULL = null stream).  Calls only enqueue
- *     work and nothing synchronises.  Nothing allocates device memory except
- *     the GEMM entry points when they split K over workgroups (few output
- *     tiles, e.g. M = 2048 at N <= 2048, or N <= 16 tokens on rows of 16 or
- *     more super-blocks): they keep one fp32 partial-sum workspace per
- *     device, allocated on first use and grown when a larger one is needed
- *     (tiles * splits * 128 KiB, resp. splits * N * M * 4 bytes), and held
- *     until exit.
+ *     work; no entry point synchronises the device or the stream.  The one
+ *     allocation is the fp32 workspace of the split launches (split-K GEMM
+ *     with few output tiles, small-batch products on long rows, decode
+ *     attention over long sequences): 48 MiB per (device, stream), made by
+ *     the first such launch on that stream, never resized or freed, so a
+ *     HIP graph captured on a stream stays valid whatever runs later, and
+ *     launches on different streams never share it.  That first allocation
+ *     is also legal while the stream is being captured.
  *   - The return value is a reflex::infer::Status value (RXQ4_STATUS_*).
  *     On an error nothing is launched; rxq4_last_error() says why.
  */
@@ -135,7 +136,7 @@ int rxq4_quantize(void *dst, int ggml_type, const float *src, int64_t n_rows, in
  * [pos][n_kv_heads][head_dim], fp16, or int8 when kv_int8 != 0 with optional
  * per-(position, KV head) fp32 scales k_scales / v_scales [pos][n_kv_heads]
  * (NULL = 1).  head_dim a multiple of 8 (int8: 16), at most 256; n_heads a
- * multiple of n_kv_heads.  Decode splits long sequences over the per-device
+ * multiple of n_kv_heads.  Decode splits long sequences over the stream's
  * workspace described above.
  * Replaces kernels::flash_attention_decode (reference attention.cu:450-466,
  * 41-173). */
@@ -152,6 +153,27 @@ int rxq4_attention_prefill_f16(void *out, const void *q, const void *k_cache,
                                const void *v_cache, int n_heads, int n_kv_heads, int head_dim,
                                int N, int start_pos, float scale, int kv_int8,
                                const float *k_scales, const float *v_scales, void *stream);
+
+/* The reference's host GEMV (gemv_quant_cpu, q4_gemm.cu:1742-1854, with its
+ * callers' output rounding: fp16 at 1898, fp32 at 2016, the residual's
+ * double rounding at 1941-1945), on HOST pointers only: y[M] = W[M x K] . x[K]
+ * for Q4_K / Q5_K / Q6_K blocks `w`, fp16 x; y_dtype F32 or F16; a non-NULL
+ * fp16 `residual` (F16 only) gives y = RNE(float(RNE(acc)) + residual).  One
+ * fp32 accumulator per row in the reference's element order, bit for bit its
+ * result.  The C++ API runs it for weights the GPU cannot read (no
+ * weights_device alias and host-only memory) and under JLLM_FAST_GEMV=0, as
+ * the reference does (q4_gemm.cu:1886-1899, 1916-1947, 1994-2016); no GPU
+ * launch ever falls back to it. */
+int rxq4_host_gemv(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
+                   const void *residual, int M, int K);
+
+/* Number of rxq4_host_gemv computations so far in this process. */
+long long rxq4_host_gemv_calls(void);
+
+/* NEW.  Allocates the split launches' workspace for `stream` on the
+ * current device now, so that no later call on that stream allocates
+ * (optional; no reference counterpart, the reference splits nothing). */
+int rxq4_reserve_workspace(void *stream);
 
 /* Pointer resolution of the reference (q4_gemm.cu:111-135): returns
  * w_device if non-NULL, else w if the HIP runtime reports it as device or

@@ -772,12 +772,6 @@ static void launch_attn_t(const AttnParams &p, dim3 grid, int hp2, bool wide, hi
     }
 }
 
-// RXQ4_ATTN_MFMA=0 keeps prefill on the VALU kernel (for comparisons).
-static bool env_attn_mfma() {
-    const char *v = getenv("RXQ4_ATTN_MFMA");
-    return !(v && v[0] == '0');
-}
-
 hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, const void *v,
                             const float *ks, const float *vs, int n_heads, int n_kv,
                             int head_dim, int n_tok, int seq0, float scale, int kv_int8,
@@ -806,20 +800,21 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
     if (n_tok == 1 && seq0 > kAttnTile) {
         // Decode: split the positions so that about 4 workgroups per CU run.
         const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-        const char *sp = getenv("RXQ4_ATTN_SPLIT");
-        const int cap = sp ? std::max(1, std::min(64, atoi(sp))) : 64;
+        int cap = tuning().attn_split ? std::min(64, tuning().attn_split) : 64;
+        // the chunk partials (n_heads x chunks x (head_dim + 2) fp32) must fit the workspace
+        const size_t per_chunk = (size_t)n_heads * (head_dim + 2) * sizeof(float);
+        cap = (int)std::min<size_t>(cap, std::max<size_t>(1, kWorkspaceBytes / per_chunk));
         const int want = std::max(1, std::min(cap, (4 * cus + units - 1) / units));
         int chunk = (seq0 + want - 1) / want;
         chunk = (chunk + kAttnTile - 1) / kAttnTile * kAttnTile;
         p.chunk = chunk;
         p.n_chunks = (seq0 + chunk - 1) / chunk;
         if (p.n_chunks > 1) {
-            const size_t bytes = (size_t)n_heads * p.n_chunks * (head_dim + 2) * sizeof(float);
-            const hipError_t e = device_workspace(bytes, &p.ws);
+            const hipError_t e = stream_workspace(st, &p.ws);
             if (e != hipSuccess) return e;
         }
     }
-    if (n_tok > 1 && (head_dim == 64 || head_dim == 128) && env_attn_mfma()) {
+    if (n_tok > 1 && (head_dim == 64 || head_dim == 128) && tuning().attn_mfma) {
         // Prefill on the matrix cores; HB = the largest power of two <= 16
         // dividing the GQA group.
         int hb = 1;

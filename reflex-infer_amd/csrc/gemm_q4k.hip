@@ -932,45 +932,6 @@ __global__ __launch_bounds__(256) void tokens_reduce_kernel(void *__restrict__ y
     store_out<YT>(y, i, s);
 }
 
-// Split-K workspace: one allocation per device on first use, grown on demand
-// (never freed).  Split-K calls that overlap on one device share it.
-struct SplitWorkspace {
-    void *ptr = nullptr;
-    size_t bytes = 0;
-};
-static std::mutex g_ws_mutex;
-static SplitWorkspace g_ws[64];
-
-hipError_t device_workspace(size_t bytes, float **ws) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    SplitWorkspace &w = g_ws[dev];
-    if (w.bytes < bytes) {
-        if (w.ptr) {
-            if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-        }
-        void *p = nullptr;
-        if ((e = hipMalloc(&p, bytes)) != hipSuccess) return e;
-        w.ptr = p;
-        w.bytes = bytes;
-    }
-    *ws = static_cast<float *>(w.ptr);
-    return hipSuccess;
-}
-
-static int env_or(const char *name, int dflt) {
-    const char *v = getenv(name);
-    if (!v || !*v) return dflt;
-    const int r = atoi(v);
-    return r > 0 ? r : dflt;
-}
-
 template <int T, int XT, int YT>
 static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
                                 int K, hipStream_t st) {
@@ -996,14 +957,16 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     // 256 CUs split 2, 172 tiles do not split.
     int splits = std::max(1, (cus + tiles / 2) / tiles);
     splits = std::min(splits, std::max(1, p.nb / 2));
-    splits = env_or("RXQ4_GEMM_SPLITS", splits);
+    if (tuning().gemm_splits) splits = tuning().gemm_splits;
+    // the fp32 partials (one 128 KiB tile per unit) must fit the workspace
+    const size_t unit_bytes = (size_t)TM * kRowsPerWg * sizeof(float);
+    splits = (int)std::min<size_t>(splits, std::max<size_t>(1, kWorkspaceBytes / (unit_bytes * tiles)));
     splits = std::max(1, std::min(splits, p.nb));
     p.sb_per_split = (p.nb + splits - 1) / splits;
     splits = (p.nb + p.sb_per_split - 1) / p.sb_per_split;  // no empty splits
     p.splits = splits;
     if (splits > 1) {
-        const size_t part = (size_t)tiles * splits * TM * kRowsPerWg * sizeof(float);
-        hipError_t e = device_workspace(part, &p.ws);
+        hipError_t e = stream_workspace(st, &p.ws);
         if (e != hipSuccess) return e;
     }
     p.total_units = tiles * splits;
@@ -1062,12 +1025,15 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
     }
     int splits = 1;
     if (t2 * kWaves < 1024 && nb >= 16) splits = std::max(1, std::min(cus / t2, nb / 8));
+    // the fp32 partials (splits x n_tok x M) must fit the workspace
+    splits = (int)std::min<size_t>(
+        splits, std::max<size_t>(1, kWorkspaceBytes / ((size_t)n_tok * M * sizeof(float))));
     if (t2 * kWaves >= 1024 || splits > 1) {
         const int sbps = (nb + splits - 1) / splits;
         splits = (nb + sbps - 1) / sbps;
         float *ws = nullptr;
         if (splits > 1) {
-            hipError_t e = device_workspace((size_t)splits * n_tok * M * sizeof(float), &ws);
+            hipError_t e = stream_workspace(st, &ws);
             if (e != hipSuccess) return e;
         }
         const dim3 grid(t2, splits);

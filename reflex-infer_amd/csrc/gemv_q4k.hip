@@ -591,13 +591,6 @@ const DeviceInfo &device_info() {
     return info;
 }
 
-static int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    if (!v || !*v) return dflt;
-    const int r = atoi(v);
-    return r > 0 ? r : dflt;
-}
-
 // Cut each range into units of `per_unit` items (an item is `rows_per_item`
 // rows); returns the unit count.  Units never straddle two ranges.
 static int assign_units(GemvParams &p, int rows_per_item, int per_unit) {
@@ -633,7 +626,7 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         // Register kernel: aim for `waves_per_cu` waves per CU over the launch.
         const int rps = 64 / slots;
         const int64_t steps = (p.total_rows + rps - 1) / rps;
-        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_WAVES_PER_CU", 4);
+        const int64_t target = (int64_t)cus * (tuning().gemv_waves_per_cu ? tuning().gemv_waves_per_cu : 4);
         int per_wave = (int)((steps + target - 1) / target);
         per_wave = std::max(1, std::min(per_wave, kRegMaxRows / rps));
         const int waves = assign_units(p, rps, per_wave);
@@ -649,7 +642,7 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         // LDS kernel: whole rows per wave, `waves_per_cu` waves per CU.
         const size_t lds = (size_t)NT * slots * kLdsSlotWords * sizeof(uint32_t);
         if (lds > 160 * 1024) return hipErrorInvalidValue;
-        const int64_t target = (int64_t)cus * env_int("RXQ4_GEMV_LDS_WAVES_PER_CU", 4);
+        const int64_t target = (int64_t)cus * (tuning().gemv_lds_waves_per_cu ? tuning().gemv_lds_waves_per_cu : 4);
         int per_wave = (int)((p.total_rows + target - 1) / target);
         if (per_wave < 1) per_wave = 1;
         const int waves = assign_units(p, 1, per_wave);
@@ -683,6 +676,12 @@ static hipError_t launch_multi_epi(GemvParams &p, int n_tok, hipStream_t st) {
         case 3: return launch_gemv_epi<EPI, 3>(p, st);
         default: return launch_gemv_epi<EPI, 4>(p, st);
     }
+}
+
+bool gemv_multi_token_fits(int n_tok, int K) {
+    const int slots = 4 * (K / 256);
+    if (slots <= 64 && (64 % slots) == 0) return true;
+    return (size_t)n_tok * slots * kLdsSlotWords * sizeof(uint32_t) <= 160 * 1024;
 }
 
 hipError_t launch_gemv_multi_token(void *y, int y_dtype, const uint8_t *w, const uint16_t *x,

@@ -41,6 +41,10 @@ constexpr int kMaxRegTokens = 4;
 // y fp16 or fp32 [n_tok x M] (token-major).
 hipError_t launch_gemv_multi_token(void *y, int y_dtype, const uint8_t *w, const uint16_t *x,
                                    int M, int n_tok, int K, hipStream_t stream);
+// Whether launch_gemv_multi_token takes n_tok tokens of length K: rows of
+// K/256 <= 16 blocks keep x in registers; longer rows stage every token's x
+// in LDS (n_tok * K/256 * 576 bytes, at most 160 KiB).
+bool gemv_multi_token_fits(int n_tok, int K);
 
 struct DeviceInfo {
     int cu_count;
@@ -87,9 +91,28 @@ hipError_t launch_kq_tokens(int ggml_type, void *y, int y_dtype, const uint8_t *
 hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
                            int64_t n_vocab, int n_ids, int K, hipStream_t stream);
 
-// The per-device fp32 workspace (split-K partials, attention chunks):
-// allocated on first use, grown with a device synchronise, held until exit.
-hipError_t device_workspace(size_t bytes, float **ws);
+// The fp32 workspace of the split launches (split-K partials, attention
+// chunks): kWorkspaceBytes per (device, stream), allocated by the first split
+// launch on that stream, never resized or freed.  Launchers choose split
+// counts whose partials fit in it.
+constexpr size_t kWorkspaceBytes = size_t(48) << 20;
+hipError_t stream_workspace(hipStream_t stream, float **ws);
+int workspace_count();  // buffers allocated so far (all devices and streams)
+
+// Tuning overrides from the environment, read once per process (for sweeps;
+// 0 / true = the launchers' defaults):
+//   RXQ4_GEMM_SPLITS, RXQ4_GEMV_WAVES_PER_CU, RXQ4_GEMV_LDS_WAVES_PER_CU,
+//   RXQ4_ATTN_SPLIT (cap on decode chunks), RXQ4_ATTN_MFMA=0 (VALU prefill),
+//   RXQ4_MULTI_TOKEN_GEMV=0 (2..4 tokens on the MFMA small-batch kernel).
+struct Tuning {
+    int gemm_splits = 0;
+    int gemv_waves_per_cu = 0;
+    int gemv_lds_waves_per_cu = 0;
+    int attn_split = 0;
+    bool attn_mfma = true;
+    bool multi_token_gemv = true;
+};
+const Tuning &tuning();
 
 // Attention for n_tok query tokens; token t sees positions [0, seq0 + t).
 // Decode is n_tok = 1, seq0 = seq_len; prefill seq0 = start_pos + 1.

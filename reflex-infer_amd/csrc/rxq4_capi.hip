@@ -1,9 +1,10 @@
 // rxq4_capi.hip -- the C ABI (include/rxq4.h) over the gfx950 launchers.
 //
 // Each entry point validates its arguments on the host, then enqueues on the
-// caller's stream.  No entry point allocates, synchronises or falls back to
-// the CPU: a call either launches the HIP kernels or returns a non-success
-// status with the reason in rxq4_last_error().
+// caller's stream.  No entry point synchronises or falls back to the CPU: a
+// call either launches the HIP kernels or returns a non-success status with
+// the reason in rxq4_last_error().  The only allocation is the split
+// launches' workspace, once per (device, stream) (runtime.cpp).
 #include "rxq4.h"
 
 #include <stdarg.h>
@@ -169,13 +170,6 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
     return from_hip(rxq4::launch_gemv(p, rxq4::kEpiF16, st), fn);
 }
 
-// RXQ4_MULTI_TOKEN_GEMV=0 sends 2..4-token products to the MFMA small-batch
-// kernel instead (for comparisons).
-static bool multi_token_gemv() {
-    const char *v = getenv("RXQ4_MULTI_TOKEN_GEMV");
-    return !(v && v[0] == '0');
-}
-
 int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x, int x_dtype,
               int M, int N, int K, void *stream) {
     const char *fn = "rxq4_gemm";
@@ -206,7 +200,8 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
     else if (kquant_type(ggml_type))
         e = rxq4::launch_gemm(ggml_type, y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype,
                               M, N, K, st);
-    else if (N <= rxq4::kMaxRegTokens && x_dtype == RXQ4_DTYPE_F16 && multi_token_gemv())
+    else if (N <= rxq4::kMaxRegTokens && x_dtype == RXQ4_DTYPE_F16 &&
+             rxq4::tuning().multi_token_gemv && rxq4::gemv_multi_token_fits(N, K))
         // 2..4 fp16 tokens: the decode GEMV with every token's activations in
         // registers (one weight read, the nibble decode shared by the tokens)
         e = rxq4::launch_gemv_multi_token(y, y_dtype, static_cast<const uint8_t *>(w),
@@ -378,6 +373,12 @@ const void *rxq4_resolve_weights(const void *w, const void *w_device) {
     }
     if (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) return w;
     return nullptr;
+}
+
+int rxq4_reserve_workspace(void *stream) {
+    float *ws = nullptr;
+    return from_hip(rxq4::stream_workspace(static_cast<hipStream_t>(stream), &ws),
+                    "rxq4_reserve_workspace");
 }
 
 const char *rxq4_version(void) { return "rxq4 0.1.0 gfx950"; }

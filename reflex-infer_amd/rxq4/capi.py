@@ -42,6 +42,10 @@ SIGNATURES = {
     "rxq4_attention_prefill_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                            c_int, c_int, c_int, ctypes.c_float, c_int, c_void_p,
                                            c_void_p, c_void_p]),
+    "rxq4_host_gemv": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p, c_int,
+                               c_int]),
+    "rxq4_host_gemv_calls": (ctypes.c_longlong, []),
+    "rxq4_reserve_workspace": (c_int, [c_void_p]),
     "rxq4_resolve_weights": (c_void_p, [c_void_p, c_void_p]),
     "rxq4_version": (ctypes.c_char_p, []),
     "rxq4_last_error": (ctypes.c_char_p, []),
@@ -179,3 +183,29 @@ def attention_prefill_f16(out, q, k, v, n_heads, n_kv_heads, head_dim, N, start_
         _ptr(out), _ptr(q), _ptr(k), _ptr(v), n_heads, n_kv_heads, head_dim, N, start_pos, scale,
         int(kv_int8), _ptr(k_scales), _ptr(v_scales), _stream(stream)),
         "rxq4_attention_prefill_f16")
+
+
+def host_gemv(w, x, M: int, K: int, ggml_type: int = GGML_TYPE_Q4_K, out: str = "f32",
+              residual=None):
+    """The host GEMV (rxq4_host_gemv) on numpy arrays: w uint8 blocks, x fp16
+    bits (uint16); out "f32" -> float32 [M], "f16" -> uint16 fp16 bits [M];
+    residual (uint16 fp16 bits [M]) gives the add variant."""
+    import numpy as np
+    w = np.ascontiguousarray(w)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    y = np.empty(M, dtype=np.float32 if out == "f32" else np.uint16)
+    res = None if residual is None else np.ascontiguousarray(residual, dtype=np.uint16)
+    _check(lib().rxq4_host_gemv(y.ctypes.data, DTYPE_F32 if out == "f32" else DTYPE_F16,
+                                w.ctypes.data, ggml_type, x.ctypes.data,
+                                None if res is None else res.ctypes.data, M, K),
+           "rxq4_host_gemv")
+    return y
+
+
+def host_gemv_calls() -> int:
+    """Computations made by the host GEMV in this process so far."""
+    return int(lib().rxq4_host_gemv_calls())
+
+
+def reserve_workspace(stream=None):
+    return _check(lib().rxq4_reserve_workspace(_stream(stream)), "rxq4_reserve_workspace")

@@ -11,12 +11,13 @@ is the caller side of that contract.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 
-from . import SUCCESS, RxQ4Error, load
+from . import NOT_IMPLEMENTED, PKG_DIR, SUCCESS, RxQ4Error, load
 
 c_void_p, c_int, c_int64, c_uint64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64
 c_char_p = ctypes.c_char_p
@@ -66,10 +67,20 @@ SIGNATURES = {
 _bound = None
 
 
+GGUF_LIB_PATH = os.path.join(PKG_DIR, "lib", "librxq4_gguf.so")
+
+
 def lib() -> ctypes.CDLL:
+    """librxq4_gguf.so (caller-side ingest, a library of its own: the
+    drop-in kernel library parses no GGUF), bound once."""
     global _bound
     if _bound is None:
-        L = load()
+        load()  # the kernel library first: ingest reports errors through it
+        if not os.path.exists(GGUF_LIB_PATH):
+            raise RxQ4Error(NOT_IMPLEMENTED, f"{GGUF_LIB_PATH} is missing; build it with "
+                            "__graft_entry__.build()")
+        L = ctypes.CDLL(GGUF_LIB_PATH)
+        L.rxq4_last_error.restype = c_char_p
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)
             fn.restype = res

@@ -27,6 +27,24 @@ def _gpu_available() -> bool:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    config.addinivalue_line("markers", "host_path: exercises the host GEMV on purpose")
+
+
+@pytest.fixture(autouse=True)
+def _gpu_tests_compute_on_the_gpu(request):
+    """A GPU test must not pass through the host GEMV (the C++ API's path for
+    weights the GPU cannot read) unless it is marked host_path."""
+    if "gpu" not in request.keywords or "host_path" in request.keywords:
+        yield
+        return
+    try:
+        from rxq4 import capi
+        before = capi.host_gemv_calls()
+    except Exception:
+        yield
+        return
+    yield
+    assert capi.host_gemv_calls() == before, "a GPU test computed through the host GEMV"
 
 
 def pytest_collection_modifyitems(config, items):

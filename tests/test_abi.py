@@ -5,8 +5,8 @@
   * the library defines every public symbol the reference's dispatcher
     defines and every kernel-seam symbol it needs
     (reference src/dispatch.cpp, src/kernels/kernel_entrypoints.h:7-16);
-  * the library exports every entry point declared in include/rxq4.h and
-    include/rxq4_gguf.h;
+  * the library exports every entry point declared in include/rxq4.h, and
+    the separate caller-side ingest library those of include/rxq4_gguf.h;
   * the reference's own dispatcher (src/dispatch.cpp compiled from its
     sources) links against the kernels-only library and its calls land in
     this build's seam (statuses the seam returns before any GPU work).
@@ -88,11 +88,26 @@ def test_reference_dispatcher_runs_on_this_kernel_layer():
                    "flash_attention_decode": 0, "registry_empty": 1}
 
 
-@pytest.mark.parametrize("header", ["rxq4.h", "rxq4_gguf.h"])
-def test_library_exports_every_c_abi_entry_point(header):
+GLIB = os.path.join(ROOT, "reflex-infer_amd", "lib", "librxq4_gguf.so")
+
+
+@pytest.mark.parametrize("header,path", [("rxq4.h", LIB), ("rxq4_gguf.h", GLIB)])
+def test_library_exports_every_c_abi_entry_point(header, path):
     text = open(os.path.join(ROOT, "include", header)).read()
     names = set(re.findall(r"\b(rxq4_[a-z0-9_]+)\s*\(", text))
+    if header != "rxq4.h":  # entry points of rxq4.h it only mentions (rxq4_last_error)
+        core = open(os.path.join(ROOT, "include", "rxq4.h")).read()
+        names -= set(re.findall(r"\b(rxq4_[a-z0-9_]+)\s*\(", core))
     assert len(names) >= 12
-    lib = ctypes.CDLL(LIB)
+    lib = ctypes.CDLL(path)
+    defined = set(_nm(path, "-D", "--defined-only"))
     for n in sorted(names):
         assert hasattr(lib, n), n
+        assert n in defined, n
+
+
+def test_drop_in_library_parses_no_gguf():
+    # reflex-infer parses no GGUF itself (docs/library-architecture.md:60):
+    # the ingest lives in its own caller-side library
+    for path in (LIB, KLIB):
+        assert not [s for s in _nm(path, "-D", "--defined-only") if "gguf" in s], path

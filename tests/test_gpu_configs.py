@@ -1,0 +1,429 @@
+"""GPU parity at the BASELINE workloads, plus the host path, the workspace
+contract and the reference's own dispatcher.
+
+  * small-batch decode on gate+up [22016 x 2048] and down
+    [2048 x 11008] with fp16 x at m = 2, 4, 8, 16 through gemm_quant_batched,
+    sampled rows against the reference semantics (per-token CPU GEMV,
+    q4_gemm.cu:1735-1739, 1742-1784) and the fp64 product of the kernel's
+    operands;
+  * the prefill GEMM on [11008 x 2048] and [2048 x 11008] at
+    m = 512 and 2048 (bf16), sampled rows against the fp64 product of
+    bf16-rounded weights;
+  * a three-layer decode chain (each layer's output feeds the next) captured
+    and replayed as a HIP graph, every projection checked against the oracle
+    on that layer's actual inputs;
+  * a graph captured on a stream keeps a valid workspace after larger split
+    launches run eagerly on that stream;
+  * weights the GPU cannot read take the reference's host path
+    (q4_gemm.cu:1886-1899, 1916-1947, 1963-1966, 1994-2016), bit for bit the
+    reference CPU loop; JLLM_FAST_GEMV=0 selects it for every call;
+  * small batches of very long rows (the multi-token GEMV's LDS limit);
+  * numeric calls through the reference's own src/dispatch.cpp, compiled from
+    its sources and linked against this build's kernel layer.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import rxq4
+from oracle import oracle as orc
+from rxq4 import api, capi
+from tests import util
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def host16(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint16)
+
+
+def f16(bits: np.ndarray) -> np.ndarray:
+    return bits.view(np.float16).astype(np.float32)
+
+
+def qweights(seed: int, rows: int, K: int, t: int = 12) -> torch.Tensor:
+    """ggml's reference quantisation of N(0, 0.02) rows, on the GPU (as bench.py)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    src = torch.randn((rows, K), generator=g, device="cuda") * 0.02
+    w = capi.quantize_ggml(src, t)
+    del src
+    return w
+
+
+def sample_rows(W: torch.Tensor, rows: np.ndarray) -> np.ndarray:
+    return W[torch.from_numpy(rows).cuda()].cpu().numpy()
+
+
+# ------------------------------------------------------------- configs[2]
+@pytest.mark.parametrize("m", [2, 4, 8, 16])
+@pytest.mark.parametrize("name,M,K", [("gate_up", 22016, 2048), ("down", 2048, 11008)])
+def test_config2_small_batch_decode(name, M, K, m):
+    print(f"configs[2] {name} [{M}x{K}] m={m}", flush=True)
+    W = qweights(2000 + M + m, M, K)
+    x16 = util.x_f16(2001 + m, (m, K))
+    x = dev(x16)
+    y = torch.empty((m, M), dtype=torch.float16, device="cuda")
+    a = api.GemmQuantBatchedArgs(y=y.data_ptr(), weights=W.data_ptr(),
+                                 weights_device=W.data_ptr(), ggml_type=12, x=x.data_ptr(),
+                                 M=M, N=m, K=K)
+    assert api.call("gemm_quant_batched", a) == rxq4.SUCCESS
+    rows = np.sort(util.rng(2002).choice(M, 384, replace=False))
+    Wn = sample_rows(W, rows)
+    got = host16(y)[:, rows]
+    ref32 = orc.gemm_tokens_f32(Wn, K, x16)       # the reference's per-token CPU GEMV
+    assert util.rel_err(f16(got), ref32) <= util.TOL
+    # the kernel's operands: up to 4 tokens the decode GEMV on exact weights
+    # (rows of 8 blocks) or its LDS variant (43 blocks), above that the MFMA
+    # kernel on fp16-rounded weights
+    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if m <= 4
+             else orc.gemm_f64(Wn, K, f16(x16), "f16"))
+    assert util.rounded_ok(got, ref64).all()
+
+
+# ------------------------------------------------------------- configs[3]
+@pytest.mark.parametrize("m", [512, 2048])
+@pytest.mark.parametrize("M,K", [(11008, 2048), (2048, 11008)])
+def test_config3_prefill_gemm(M, K, m):
+    print(f"configs[3] [{M}x{K}] m={m}", flush=True)
+    W = qweights(3000 + M + m, M, K)
+    g = torch.Generator(device="cuda").manual_seed(3001 + m)
+    x = torch.randn((m, K), generator=g, device="cuda").to(torch.bfloat16)
+    yb = torch.empty((m, M), dtype=torch.bfloat16, device="cuda")
+    capi.gemm(yb, W, x, M, m, K)
+    y32 = torch.empty((m, M), dtype=torch.float32, device="cuda")
+    capi.gemm(y32, W, x, M, m, K)
+    rows = np.sort(util.rng(3002).choice(M, 128, replace=False))
+    Wn = sample_rows(W, rows)
+    # fp64 product of the kernel's operands: bf16(dequant(w)) and bf16 x
+    wb = orc.bits_bf16_to_f32(orc.dequant_bf16(Wn, K)).astype(np.float64).reshape(len(rows), K)
+    ref = x.float().cpu().numpy().astype(np.float64) @ wb.T
+    assert util.rel_err(y32.cpu().numpy()[:, rows], ref) <= util.TOL
+    got = yb.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows]
+    assert util.rounded_ok(got, ref, "bf16").all()
+    # spot-check the fp64 shortcut against the oracle's own GEMM on 8 rows
+    ref8 = orc.gemm_f64(Wn[:8], K, x[:64].float().cpu().numpy(), "bf16")
+    assert np.allclose(ref8, ref[:64, :8], rtol=0, atol=1e-9 * np.abs(ref).max())
+
+
+# ------------------------------------------------------ a decode layer chain
+def test_decode_chain_three_layers_in_a_graph():
+    """h -> QKV triple(h); o = O(h) + h; gu = gate+up(o); h' = down(gu[:FFN]) + o,
+    three layers captured once and replayed; each projection is checked
+    against the oracle on the inputs the GPU actually fed it."""
+    H, F, L = 2048, 11008, 3
+    Ms = (2048, 256, 256)
+    Ws = [{"qkv": qweights(4000 + 10 * l, sum(Ms), H), "o": qweights(4001 + 10 * l, H, H),
+           "gu": qweights(4002 + 10 * l, 2 * F, H), "down": qweights(4003 + 10 * l, H, F)}
+          for l in range(L)]
+    h = [torch.empty(H, dtype=torch.float16, device="cuda") for _ in range(L + 1)]
+    h[0].copy_(torch.from_numpy(util.gaussian(4100, H)).half())
+    qkv = [torch.empty(sum(Ms), dtype=torch.float16, device="cuda") for _ in range(L)]
+    o = [torch.empty(H, dtype=torch.float16, device="cuda") for _ in range(L)]
+    gu = [torch.empty(2 * F, dtype=torch.float16, device="cuda") for _ in range(L)]
+    rb = (H // 256) * 144
+    s = torch.cuda.Stream()
+
+    def layers():
+        sp = s.cuda_stream
+        for l in range(L):
+            q = Ws[l]["qkv"].data_ptr()
+            a = api.GemvQuantTripleArgs(
+                y0=qkv[l].data_ptr(), weights0=q, weights0_device=q, ggml_type0=12, M0=Ms[0],
+                y1=qkv[l].data_ptr() + 2 * Ms[0], weights1=q + Ms[0] * rb,
+                weights1_device=q + Ms[0] * rb, ggml_type1=12, M1=Ms[1],
+                y2=qkv[l].data_ptr() + 2 * (Ms[0] + Ms[1]), weights2=q + (Ms[0] + Ms[1]) * rb,
+                weights2_device=q + (Ms[0] + Ms[1]) * rb, ggml_type2=12, M2=Ms[2],
+                x=h[l].data_ptr(), K=H, stream=sp)
+            assert api.call("gemv_quant_triple", a) == rxq4.SUCCESS
+            a = api.GemvQuantAddArgs(y=o[l].data_ptr(), weights=Ws[l]["o"].data_ptr(),
+                                     weights_device=Ws[l]["o"].data_ptr(), ggml_type=12,
+                                     x=h[l].data_ptr(), residual=h[l].data_ptr(), M=H, K=H,
+                                     stream=sp)
+            assert api.call("gemv_quant_add", a) == rxq4.SUCCESS
+            g = Ws[l]["gu"].data_ptr()
+            a = api.GemvQuantPairArgs(y0=gu[l].data_ptr(), weights0=g, weights0_device=g,
+                                      ggml_type0=12, M0=F, y1=gu[l].data_ptr() + 2 * F,
+                                      weights1=g + F * rb, weights1_device=g + F * rb,
+                                      ggml_type1=12, M1=F, x=o[l].data_ptr(), K=H, stream=sp)
+            assert api.call("gemv_quant_pair", a) == rxq4.SUCCESS
+            a = api.GemvQuantAddArgs(y=h[l + 1].data_ptr(), weights=Ws[l]["down"].data_ptr(),
+                                     weights_device=Ws[l]["down"].data_ptr(), ggml_type=12,
+                                     x=gu[l].data_ptr(), residual=o[l].data_ptr(), M=H, K=F,
+                                     stream=sp)
+            assert api.call("gemv_quant_add", a) == rxq4.SUCCESS
+
+    with torch.cuda.stream(s):
+        layers()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in h + qkv + o + gu]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        layers()
+    for t in h[1:] + qkv + o + gu:
+        t.fill_(0)
+    graph.replay()
+    torch.cuda.synchronize()
+    for a, b in zip(h + qkv + o + gu, eager):
+        assert torch.equal(a, b)
+    for l in range(L):
+        hl = host16(h[l])
+        Wq = Ws[l]["qkv"].cpu().numpy()
+        assert util.rounded_ok(host16(qkv[l]), orc.gemv_f32(Wq, H, hl)).all(), l
+        Wo = Ws[l]["o"].cpu().numpy()
+        y32 = orc.gemv_f32(Wo, H, hl)
+        sp = util.spacing(orc.f32_to_fp16(y32), "f16")
+        assert util.rounded_ok(host16(o[l]), y32.astype(np.float64) + f16(hl),
+                               extra=sp / 2).all(), l
+        ol = host16(o[l])
+        assert util.rounded_ok(host16(gu[l]), orc.gemv_f32(Ws[l]["gu"].cpu().numpy(), H, ol)).all()
+        gl = host16(gu[l])[:F]
+        yd = orc.gemv_f32(Ws[l]["down"].cpu().numpy(), F, gl)
+        sp = util.spacing(orc.f32_to_fp16(yd), "f16")
+        assert util.rounded_ok(host16(h[l + 1]), yd.astype(np.float64) + f16(ol),
+                               extra=sp / 2).all(), l
+        assert np.isfinite(f16(host16(h[l + 1]))).all()
+
+
+# ------------------------------------------------------------- workspace
+def test_graph_workspace_survives_later_split_launches():
+    """Capture split-KV decode attention (small workspace use) on a fresh
+    stream -- its workspace is allocated during the capture -- then run a
+    large split-K GEMM and split small-batch products eagerly on the same
+    stream and on another, and replay: every replay equals the eager result."""
+    H, KV, D, S = 32, 8, 128, 4096
+    g = torch.Generator(device="cuda").manual_seed(5000)
+    k = (torch.randn((S, KV, D), generator=g, device="cuda")).half()
+    v = (torch.randn((S, KV, D), generator=g, device="cuda")).half()
+    q = torch.randn(H * D, generator=g, device="cuda").half()
+    ref = torch.empty(H * D, dtype=torch.float16, device="cuda")
+    capi.attention_decode_f16(ref, q, k, v, H, KV, D, S, D ** -0.5)
+    s = torch.cuda.Stream()
+    out = torch.empty_like(ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        capi.attention_decode_f16(out, q, k, v, H, KV, D, S, D ** -0.5, stream=s)
+    M, N, K = 2048, 512, 11008
+    W = qweights(5001, M, K)
+    x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+    y2 = torch.empty_like(y)
+    xs = torch.randn((16, K), generator=g, device="cuda").half()
+    ys = torch.empty((16, M), dtype=torch.float16, device="cuda")
+    for rep in range(3):
+        out.fill_(0)
+        with torch.cuda.stream(s):
+            capi.gemm(y, W, x, M, N, K, stream=s)          # split-K, 32 MiB of partials
+            capi.gemm_f16(ys, W, xs, M, 16, K, stream=s)   # split small batch
+            graph.replay()
+        capi.gemm(y2, W, x, M, N, K)                       # another stream
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), rep
+        assert torch.equal(y, y2), rep
+
+
+def test_reserve_workspace():
+    s = torch.cuda.Stream()
+    capi.reserve_workspace(s)
+    capi.reserve_workspace(s)  # idempotent
+
+
+# ------------------------------------------------------------- host path
+@pytest.mark.host_path
+@pytest.mark.parametrize("t", [12, 13, 14])
+def test_host_only_weights_take_the_reference_host_path(t):
+    M, K = 300, 2048
+    src = util.gaussian(6000 + t, (M, K), 0.02)
+    Wn = orc.quantize(src) if t == 12 else orc.quantize_ggml(src, t)
+    x16, res16 = util.x_f16(6001, K), util.x_f16(6002, M)
+    x, res = dev(x16), dev(res16)
+    y = torch.empty(M, dtype=torch.float16, device="cuda")
+    n0 = capi.host_gemv_calls()
+    a = api.GemvQuantArgs(y=y.data_ptr(), weights=Wn.ctypes.data, ggml_type=t, x=x.data_ptr(),
+                          M=M, K=K)
+    assert api.call("gemv_quant", a) == rxq4.SUCCESS
+    ref32 = orc.gemv_f32(Wn, K, x16) if t == 12 else orc.kq_gemv_f32(Wn, K, t, x16)
+    assert np.array_equal(host16(y), ref32.astype(np.float16).view(np.uint16))
+    a = api.GemvQuantAddArgs(y=y.data_ptr(), weights=Wn.ctypes.data, ggml_type=t,
+                             x=x.data_ptr(), residual=res.data_ptr(), M=M, K=K)
+    assert api.call("gemv_quant_add", a) == rxq4.SUCCESS
+    expect = (f16(ref32.astype(np.float16).view(np.uint16)) + f16(res16)).astype(np.float16)
+    assert np.array_equal(host16(y), expect.view(np.uint16))
+    y32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    a = api.GemvQuantF32Args(y=y32.data_ptr(), weights=Wn.ctypes.data, ggml_type=t,
+                             x=x.data_ptr(), M=M, K=K)
+    assert api.call("gemv_quant_f32", a) == rxq4.SUCCESS
+    assert np.array_equal(y32.cpu().numpy().view(np.uint32), ref32.view(np.uint32))
+    assert capi.host_gemv_calls() == n0 + 3
+
+
+@pytest.mark.host_path
+def test_host_path_per_range_and_per_token():
+    K = 2048
+    x16 = util.x_f16(6100, (3, K))
+    x = dev(x16)
+    W0n, W1n = util.weights(6101, 64, K), util.weights(6102, 40, K)
+    W0 = dev(W0n)
+    y0 = torch.empty(64, dtype=torch.float16, device="cuda")
+    y1 = torch.empty(40, dtype=torch.float16, device="cuda")
+    n0 = capi.host_gemv_calls()
+    # pair: range 0 on the GPU, range 1 host-only (per-range fallback)
+    a = api.GemvQuantPairArgs(y0=y0.data_ptr(), weights0=W0.data_ptr(), ggml_type0=12, M0=64,
+                              y1=y1.data_ptr(), weights1=W1n.ctypes.data, ggml_type1=12, M1=40,
+                              x=x.data_ptr(), K=K)
+    assert api.call("gemv_quant_pair", a) == rxq4.SUCCESS
+    assert util.rounded_ok(host16(y0), orc.gemv_f32(W0n, K, x16[0])).all()
+    assert np.array_equal(host16(y1), orc.gemv_f16(W1n, K, x16[0]))
+    assert capi.host_gemv_calls() == n0 + 1
+    # triple, all host-only, mixed Q4_K / Q4_K / Q6_K
+    W2n = orc.quantize_ggml(util.gaussian(6103, (16, K), 0.02), 14)
+    ys = [torch.empty(m, dtype=torch.float16, device="cuda") for m in (64, 40, 16)]
+    a = api.GemvQuantTripleArgs(
+        y0=ys[0].data_ptr(), weights0=W0n.ctypes.data, ggml_type0=12, M0=64,
+        y1=ys[1].data_ptr(), weights1=W1n.ctypes.data, ggml_type1=12, M1=40,
+        y2=ys[2].data_ptr(), weights2=W2n.ctypes.data, ggml_type2=14, M2=16,
+        x=x.data_ptr(), K=K)
+    assert api.call("gemv_quant_triple", a) == rxq4.SUCCESS
+    assert np.array_equal(host16(ys[0]), orc.gemv_f16(W0n, K, x16[0]))
+    assert np.array_equal(host16(ys[1]), orc.gemv_f16(W1n, K, x16[0]))
+    ref2 = orc.kq_gemv_f32(W2n, K, 14, x16[0]).astype(np.float16).view(np.uint16)
+    assert np.array_equal(host16(ys[2]), ref2)
+    # batched GEMM on host-only weights: one host GEMV per token
+    yb = torch.empty((3, 40), dtype=torch.float16, device="cuda")
+    a = api.GemmQuantBatchedArgs(y=yb.data_ptr(), weights=W1n.ctypes.data, ggml_type=12,
+                                 x=x.data_ptr(), M=40, N=3, K=K)
+    assert api.call("gemm_quant_batched", a) == rxq4.SUCCESS
+    for t in range(3):
+        assert np.array_equal(host16(yb[t]), orc.gemv_f16(W1n, K, x16[t]))
+    # the embedding has no host path (reference q4_gemm.cu:2083-2087)
+    e = api.DequantEmbeddingRowArgs(dst=y0.data_ptr(), weights=W0n.ctypes.data, ggml_type=12,
+                                    token_id=0, hidden_dim=K)
+    assert api.call("dequant_embedding_row", e) == rxq4.INVALID_ARGUMENT
+
+
+FAST_GEMV_OFF = r"""
+import sys, numpy as np, torch
+sys.path[:0] = [ROOT, ROOT + "/reflex-infer_amd"]
+import rxq4
+from rxq4 import api, capi
+from oracle import oracle as orc
+from tests import util
+M, K = 128, 2048
+Wn = util.weights(6200, M, K)
+W = torch.from_numpy(Wn).cuda()
+x16 = util.x_f16(6201, K)
+x = torch.from_numpy(x16.view(np.int16)).cuda()
+y = torch.empty(M, dtype=torch.float16, device="cuda")
+a = api.GemvQuantArgs(y=y.data_ptr(), weights=Wn.ctypes.data, weights_device=W.data_ptr(),
+                      ggml_type=12, x=x.data_ptr(), M=M, K=K)
+assert api.call("gemv_quant", a) == rxq4.SUCCESS
+assert np.array_equal(y.cpu().numpy().view(np.uint16), orc.gemv_f16(Wn, K, x16))
+assert capi.host_gemv_calls() == 1
+print("fast-gemv-off ok")
+"""
+
+
+@pytest.mark.host_path
+def test_jllm_fast_gemv_0_selects_the_host_path():
+    env = dict(os.environ, JLLM_FAST_GEMV="0")
+    r = subprocess.run([sys.executable, "-c", FAST_GEMV_OFF.replace("ROOT", repr(ROOT))],
+                       env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "fast-gemv-off ok" in r.stdout
+
+
+# --------------------------------------------------- very long rows, m <= 4
+@pytest.mark.parametrize("M,N,K", [(64, 4, 28672), (64, 3, 24320), (64, 2, 65536),
+                                   (64, 4, 16384)])
+def test_small_batch_long_rows(M, N, K):
+    print(f"small batch long rows M={M} N={N} K={K}", flush=True)
+    Wn = util.weights(7000 + N + K // 256, M, K)
+    x16 = util.x_f16(7001 + N, (N, K))
+    W, x = dev(Wn), dev(x16)
+    y = torch.empty((N, M), dtype=torch.float16, device="cuda")
+    a = api.GemmQuantBatchedArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=12,
+                                 x=x.data_ptr(), M=M, N=N, K=K)
+    assert api.call("gemm_quant_batched", a) == rxq4.SUCCESS
+    ref32 = orc.gemm_tokens_f32(Wn, K, x16)
+    assert util.rel_err(f16(host16(y)), ref32) <= util.TOL
+    # the multi-token GEMV stages N rows of x in LDS (N * K/256 * 576 bytes);
+    # past 160 KiB the MFMA small-batch kernel (fp16 weight tiles) takes over
+    fits = N * (K // 256) * 576 <= 160 * 1024
+    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if fits
+             else orc.gemm_f64(Wn, K, f16(x16), "f16"))
+    assert util.rounded_ok(host16(y), ref64).all()
+
+
+# ------------------------------------------------- the reference dispatcher
+REF_DISPATCH = os.path.join(ROOT, "oracle", "_ref", "libdispatch_ref_on_hip.so")
+
+
+@pytest.mark.skipif(not os.path.exists(REF_DISPATCH),
+                    reason="reference dispatcher not built (needs the reference checkout)")
+def test_reference_dispatcher_computes_on_this_kernel_layer():
+    """reflex::infer::* as defined by the reference's src/dispatch.cpp (its
+    object, not this build's dispatcher), over this build's seam and HIP
+    kernels: GEMV, add, pair, f32 and the embedding row against the oracle."""
+    ref = ctypes.CDLL(REF_DISPATCH)
+    ours = rxq4.load()
+    sym = api.SYMBOLS["gemv_quant"][0]
+    assert (ctypes.cast(getattr(ref, sym), ctypes.c_void_p).value !=
+            ctypes.cast(getattr(ours, sym), ctypes.c_void_p).value)
+
+    def call(name, args):
+        s, argt = api.SYMBOLS[name]
+        f = getattr(ref, s)
+        f.restype = ctypes.c_uint8
+        f.argtypes = [ctypes.POINTER(argt)]
+        return int(f(ctypes.byref(args)))
+
+    M, K = 512, 2048
+    Wn = util.weights(8000, M, K)
+    x16, res16 = util.x_f16(8001, K), util.x_f16(8002, M)
+    W, x, res = dev(Wn), dev(x16), dev(res16)
+    ref32 = orc.gemv_f32(Wn, K, x16)
+    y = torch.empty(M, dtype=torch.float16, device="cuda")
+    assert call("gemv_quant", api.GemvQuantArgs(y=y.data_ptr(), weights=W.data_ptr(),
+                                                ggml_type=12, x=x.data_ptr(), M=M, K=K)) == 0
+    torch.cuda.synchronize()
+    assert util.rounded_ok(host16(y), ref32).all()
+    y32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    assert call("gemv_quant_f32", api.GemvQuantF32Args(y=y32.data_ptr(), weights=W.data_ptr(),
+                                                       ggml_type=12, x=x.data_ptr(), M=M,
+                                                       K=K)) == 0
+    torch.cuda.synchronize()
+    assert util.rel_err(y32.cpu().numpy(), ref32) <= util.TOL
+    assert call("gemv_quant_add", api.GemvQuantAddArgs(
+        y=y.data_ptr(), weights=W.data_ptr(), ggml_type=12, x=x.data_ptr(),
+        residual=res.data_ptr(), M=M, K=K)) == 0
+    torch.cuda.synchronize()
+    assert util.rel_err(f16(host16(y)), f16(orc.gemv_add_f16(Wn, K, x16, res16))) <= util.TOL
+    y0 = torch.empty(300, dtype=torch.float16, device="cuda")
+    y1 = torch.empty(212, dtype=torch.float16, device="cuda")
+    row = (K // 256) * 144
+    assert call("gemv_quant_pair", api.GemvQuantPairArgs(
+        y0=y0.data_ptr(), weights0=W.data_ptr(), ggml_type0=12, M0=300,
+        y1=y1.data_ptr(), weights1=W.data_ptr() + 300 * row, ggml_type1=12, M1=212,
+        x=x.data_ptr(), K=K)) == 0
+    torch.cuda.synchronize()
+    assert util.rounded_ok(np.concatenate([host16(y0), host16(y1)]), ref32).all()
+    e = torch.empty(K, dtype=torch.float16, device="cuda")
+    assert call("dequant_embedding_row", api.DequantEmbeddingRowArgs(
+        dst=e.data_ptr(), weights=W.data_ptr(), ggml_type=12, token_id=77, hidden_dim=K)) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(host16(e), orc.dequant_f16(Wn, K, 77, 1)[0])

@@ -210,9 +210,11 @@ def test_pair_on_long_rows():
         assert util.rounded_ok(host16(yv), orc.gemv_f32(Wn, K, x16)).all()
 
 
+@pytest.mark.host_path
 def test_api_gemv_pointer_resolution():
     """weights_device alias wins over a host `weights` pointer; a device
-    `weights` pointer resolves by itself; host memory alone is rejected."""
+    `weights` pointer resolves by itself; host memory alone takes the
+    reference's host path (q4_gemm.cu:1886-1899), bit for bit its CPU loop."""
     M, K = 256, 2048
     Wn = util.weights(80, M, K)
     x16 = util.x_f16(81, K)
@@ -229,9 +231,12 @@ def test_api_gemv_pointer_resolution():
                           M=M, K=K)
     assert api.call("gemv_quant", a) == rxq4.SUCCESS
     assert util.rounded_ok(host16(y), ref).all()
+    n0 = capi.host_gemv_calls()
     a = api.GemvQuantArgs(y=y.data_ptr(), weights=host_ptr, ggml_type=12, x=x.data_ptr(),
                           M=M, K=K)
-    assert api.call("gemv_quant", a) == rxq4.INVALID_ARGUMENT
+    assert api.call("gemv_quant", a) == rxq4.SUCCESS
+    assert np.array_equal(host16(y), orc.gemv_f16(Wn, K, x16))
+    assert capi.host_gemv_calls() == n0 + 1
     a = api.GemvQuantArgs(y=y.data_ptr(), weights=W.data_ptr(), ggml_type=15, x=x.data_ptr(),
                           M=M, K=K)
     assert api.call("gemv_quant", a) == rxq4.UNSUPPORTED_QUANT_FORMAT
