@@ -810,7 +810,8 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
         p.chunk = chunk;
         p.n_chunks = (seq0 + chunk - 1) / chunk;
         if (p.n_chunks > 1) {
-            const hipError_t e = stream_workspace(st, &p.ws);
+            const hipError_t e =
+                Scratch{}.get(st, per_chunk * p.n_chunks, &p.ws);
             if (e != hipSuccess) return e;
         }
     }

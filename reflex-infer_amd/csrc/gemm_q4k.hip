@@ -934,7 +934,7 @@ __global__ __launch_bounds__(256) void tokens_reduce_kernel(void *__restrict__ y
 
 template <int T, int XT, int YT>
 static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
-                                int K, hipStream_t st) {
+                                int K, hipStream_t st, const Scratch &sc) {
     constexpr int TM = 128;  // tokens per workgroup tile
     // 32-bit buffer offsets: the x tile, and a wave's 32 rows of Q6_K weights
     const int64_t row_bytes = (int64_t)(K / 256) * GemmFmt<T>::kBytes;
@@ -958,15 +958,15 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     int splits = std::max(1, (cus + tiles / 2) / tiles);
     splits = std::min(splits, std::max(1, p.nb / 2));
     if (tuning().gemm_splits) splits = tuning().gemm_splits;
-    // the fp32 partials (one 128 KiB tile per unit) must fit the workspace
+    // the fp32 partials (one 128 KiB tile per unit) must fit the scratch
     const size_t unit_bytes = (size_t)TM * kRowsPerWg * sizeof(float);
-    splits = (int)std::min<size_t>(splits, std::max<size_t>(1, kWorkspaceBytes / (unit_bytes * tiles)));
+    splits = (int)std::min<size_t>(splits, std::max<size_t>(1, sc.capacity() / (unit_bytes * tiles)));
     splits = std::max(1, std::min(splits, p.nb));
     p.sb_per_split = (p.nb + splits - 1) / splits;
     splits = (p.nb + p.sb_per_split - 1) / p.sb_per_split;  // no empty splits
     p.splits = splits;
     if (splits > 1) {
-        hipError_t e = stream_workspace(st, &p.ws);
+        hipError_t e = sc.get(st, unit_bytes * tiles * splits, &p.ws);
         if (e != hipSuccess) return e;
     }
     p.total_units = tiles * splits;
@@ -980,28 +980,29 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
 
 template <int T>
 static hipError_t launch_gemm_xy(void *y, int y_dtype, const uint8_t *w, const void *x,
-                                 int x_dtype, int M, int N, int K, hipStream_t st) {
+                                 int x_dtype, int M, int N, int K, hipStream_t st,
+                                 const Scratch &sc) {
     const uint16_t *xx = static_cast<const uint16_t *>(x);
     if (x_dtype == RXQ4_DTYPE_BF16) {
         if (y_dtype == RXQ4_DTYPE_BF16)
-            return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, N, K, st);
-        return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
+            return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, N, K, st, sc);
+        return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st, sc);
     }
     if (y_dtype == RXQ4_DTYPE_F16)
-        return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, N, K, st);
-    return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st);
+        return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, N, K, st, sc);
+    return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st, sc);
 }
 
 hipError_t launch_gemm(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,
-                       int x_dtype, int M, int N, int K, hipStream_t st) {
-    if (ggml_type == 14) return launch_gemm_xy<14>(y, y_dtype, w, x, x_dtype, M, N, K, st);
-    if (ggml_type == 13) return launch_gemm_xy<13>(y, y_dtype, w, x, x_dtype, M, N, K, st);
-    return launch_gemm_xy<12>(y, y_dtype, w, x, x_dtype, M, N, K, st);
+                       int x_dtype, int M, int N, int K, hipStream_t st, const Scratch &sc) {
+    if (ggml_type == 14) return launch_gemm_xy<14>(y, y_dtype, w, x, x_dtype, M, N, K, st, sc);
+    if (ggml_type == 13) return launch_gemm_xy<13>(y, y_dtype, w, x, x_dtype, M, N, K, st, sc);
+    return launch_gemm_xy<12>(y, y_dtype, w, x, x_dtype, M, N, K, st, sc);
 }
 
 template <int XT, int YT>
 static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, int M, int n_tok,
-                                  int K, hipStream_t st) {
+                                  int K, hipStream_t st, const Scratch &sc) {
     // Four waves split K.  Two row tiles per wave halve the x traffic per
     // weight byte and pay off once there are enough of them to give about
     // four waves per CU (1024 waves); a measured sweep of 1/2/4 row tiles and
@@ -1025,15 +1026,15 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
     }
     int splits = 1;
     if (t2 * kWaves < 1024 && nb >= 16) splits = std::max(1, std::min(cus / t2, nb / 8));
-    // the fp32 partials (splits x n_tok x M) must fit the workspace
+    // the fp32 partials (splits x n_tok x M) must fit the scratch
     splits = (int)std::min<size_t>(
-        splits, std::max<size_t>(1, kWorkspaceBytes / ((size_t)n_tok * M * sizeof(float))));
+        splits, std::max<size_t>(1, sc.capacity() / ((size_t)n_tok * M * sizeof(float))));
     if (t2 * kWaves >= 1024 || splits > 1) {
         const int sbps = (nb + splits - 1) / splits;
         splits = (nb + sbps - 1) / sbps;
         float *ws = nullptr;
         if (splits > 1) {
-            hipError_t e = stream_workspace(st, &ws);
+            hipError_t e = sc.get(st, (size_t)splits * n_tok * M * sizeof(float), &ws);
             if (e != hipSuccess) return e;
         }
         const dim3 grid(t2, splits);
@@ -1060,16 +1061,17 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
 }
 
 hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void *x,
-                              int x_dtype, int M, int n_tok, int K, hipStream_t st) {
+                              int x_dtype, int M, int n_tok, int K, hipStream_t st,
+                              const Scratch &sc) {
     const uint16_t *xx = static_cast<const uint16_t *>(x);
     if (x_dtype == RXQ4_DTYPE_BF16) {
         if (y_dtype == RXQ4_DTYPE_BF16)
-            return launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, n_tok, K, st);
-        return launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
+            return launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, n_tok, K, st, sc);
+        return launch_tokens_t<RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st, sc);
     }
     if (y_dtype == RXQ4_DTYPE_F16)
-        return launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, n_tok, K, st);
-    return launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st);
+        return launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, n_tok, K, st, sc);
+    return launch_tokens_t<RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, n_tok, K, st, sc);
 }
 
 }  // namespace rxq4

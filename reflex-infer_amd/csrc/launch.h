@@ -7,6 +7,33 @@
 
 namespace rxq4 {
 
+// The fp32 workspace of the split launches (split-K partials, attention
+// chunks): kWorkspaceBytes per (device, stream), allocated by the first split
+// launch on that stream, never resized or freed.  Launchers choose split
+// counts whose partials fit in it.
+constexpr size_t kWorkspaceBytes = size_t(48) << 20;
+hipError_t stream_workspace(hipStream_t stream, float **ws);
+
+// Where a split launch keeps its fp32 partials: `ptr` (device memory of
+// `bytes` bytes, supplied by the caller) or, when ptr is null, the stream's
+// workspace above.
+struct Scratch {
+    float *ptr = nullptr;
+    size_t bytes = 0;
+    size_t capacity() const { return ptr ? bytes : kWorkspaceBytes; }
+    // `need` bytes of it; launchers size their splits to fit, so a request
+    // beyond the capacity is a launcher bug and fails without a launch
+    hipError_t get(hipStream_t st, size_t need, float **p) const {
+        if (need > capacity()) return hipErrorInvalidValue;
+        if (ptr) {
+            *p = ptr;
+            return hipSuccess;
+        }
+        return stream_workspace(st, p);
+    }
+};
+int workspace_count();  // buffers allocated so far (all devices and streams)
+
 enum Epilogue : int { kEpiF16 = 0, kEpiF32 = 1, kEpiAdd = 2 };
 
 // One output range of a (multi-)GEMV: rows of `w` produce y[0 .. rows).
@@ -62,13 +89,15 @@ hipError_t launch_gemv(GemvParams p, int epilogue, hipStream_t stream);
 // y[t*M + row] (fp16 or fp32) = W[row] . x[t].
 constexpr int kMaxSmallBatch = 16;
 hipError_t launch_gemv_tokens(void *y, int y_dtype, const uint8_t *w, const void *x,
-                              int x_dtype, int M, int n_tok, int K, hipStream_t stream);
+                              int x_dtype, int M, int n_tok, int K, hipStream_t stream,
+                              const Scratch &sc = Scratch{});
 
 // MFMA GEMM: y[N x M] = x[N x K] . dequant(W)^T for Q4_K (12), Q5_K (13)
 // or Q6_K (14) weights, with x/weight tiles of the x type (fp16 or bf16) and
 // fp32 accumulation; y fp32/fp16/bf16.
 hipError_t launch_gemm(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,
-                       int x_dtype, int M, int N, int K, hipStream_t stream);
+                       int x_dtype, int M, int N, int K, hipStream_t stream,
+                       const Scratch &sc = Scratch{});
 
 // Embedding rows: dst[i, :] = fp16(dequant(W[id_i, :])).  ids == nullptr means
 // the single row token_id (no range check, as in the reference).
@@ -91,13 +120,6 @@ hipError_t launch_kq_tokens(int ggml_type, void *y, int y_dtype, const uint8_t *
 hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
                            int64_t n_vocab, int n_ids, int K, hipStream_t stream);
 
-// The fp32 workspace of the split launches (split-K partials, attention
-// chunks): kWorkspaceBytes per (device, stream), allocated by the first split
-// launch on that stream, never resized or freed.  Launchers choose split
-// counts whose partials fit in it.
-constexpr size_t kWorkspaceBytes = size_t(48) << 20;
-hipError_t stream_workspace(hipStream_t stream, float **ws);
-int workspace_count();  // buffers allocated so far (all devices and streams)
 
 // Tuning overrides from the environment, read once per process (for sweeps;
 // 0 / true = the launchers' defaults):

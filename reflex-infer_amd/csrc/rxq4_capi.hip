@@ -170,9 +170,14 @@ int rxq4_gemv_multi_f16(const rxq4_rows *ranges, int n_ranges, const void *x, in
     return from_hip(rxq4::launch_gemv(p, rxq4::kEpiF16, st), fn);
 }
 
-int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x, int x_dtype,
-              int M, int N, int K, void *stream) {
-    const char *fn = "rxq4_gemm";
+}  // extern "C"
+
+namespace {
+
+// The GEMM routing shared by rxq4_gemm and rxq4_gemm_noalloc; split launches
+// keep their partials in `sc`.
+int gemm_impl(const char *fn, void *y, int y_dtype, const void *w, int ggml_type, const void *x,
+              int x_dtype, int M, int N, int K, void *stream, const rxq4::Scratch &sc) {
     int s = check_common(fn, w, ggml_type, K);
     if (s != RXQ4_STATUS_SUCCESS) return s;
     if ((s = check_x(fn, x)) != RXQ4_STATUS_SUCCESS) return s;
@@ -199,7 +204,7 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
                                    x_dtype, M, N, K, st);
     else if (kquant_type(ggml_type))
         e = rxq4::launch_gemm(ggml_type, y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype,
-                              M, N, K, st);
+                              M, N, K, st, sc);
     else if (N <= rxq4::kMaxRegTokens && x_dtype == RXQ4_DTYPE_F16 &&
              rxq4::tuning().multi_token_gemv && rxq4::gemv_multi_token_fits(N, K))
         // 2..4 fp16 tokens: the decode GEMV with every token's activations in
@@ -208,11 +213,21 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
                                           static_cast<const uint16_t *>(x), M, N, K, st);
     else if (N <= rxq4::kMaxSmallBatch)
         e = rxq4::launch_gemv_tokens(y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M,
-                                     N, K, st);
+                                     N, K, st, sc);
     else
         e = rxq4::launch_gemm(12, y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype, M, N, K,
-                              st);
+                              st, sc);
     return from_hip(e, fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x, int x_dtype,
+              int M, int N, int K, void *stream) {
+    return gemm_impl("rxq4_gemm", y, y_dtype, w, ggml_type, x, x_dtype, M, N, K, stream,
+                     rxq4::Scratch{});
 }
 
 int rxq4_gemm_f16(void *y, const void *w, int ggml_type, const void *x, int M, int N, int K,

@@ -168,6 +168,7 @@ def test_decode_chain_three_layers_in_a_graph():
                                      stream=sp)
             assert api.call("gemv_quant_add", a) == rxq4.SUCCESS
 
+    torch.cuda.synchronize()  # inputs were made on the default stream
     with torch.cuda.stream(s):
         layers()
     torch.cuda.synchronize()
@@ -177,7 +178,9 @@ def test_decode_chain_three_layers_in_a_graph():
         layers()
     for t in h[1:] + qkv + o + gu:
         t.fill_(0)
-    graph.replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        graph.replay()
     torch.cuda.synchronize()
     for a, b in zip(h + qkv + o + gu, eager):
         assert torch.equal(a, b)
@@ -225,9 +228,10 @@ def test_graph_workspace_survives_later_split_launches():
     y2 = torch.empty_like(y)
     xs = torch.randn((16, K), generator=g, device="cuda").half()
     ys = torch.empty((16, M), dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()  # the inputs come from the default stream; s does not wait for it
     for rep in range(3):
-        out.fill_(0)
         with torch.cuda.stream(s):
+            out.fill_(0)
             capi.gemm(y, W, x, M, N, K, stream=s)          # split-K, 32 MiB of partials
             capi.gemm_f16(ys, W, xs, M, 16, K, stream=s)   # split small batch
             graph.replay()
