@@ -31,8 +31,17 @@ stream and timed with HIP events recorded on that stream around replays:
   small_batch_decode  m in {1,2,4,8,16} tokens on gate+up and down
                (where weight reuse ends the purely
                bandwidth-bound regime)
+  floors       what the box gives a launch and a stream: an empty kernel
+               per graph launch, and a pure 16-byte streaming read of each
+               decode projection's bytes (distinct buffers per launch), the
+               ceilings the GEMV kernels are judged against
   cpu_baseline the oracle's restatement of the reference CPU GEMV
-               (gemv_quant_cpu) over the full 36-layer set, single thread.
+               (gemv_quant_cpu) over the full 36-layer set, single thread
+               (median of 5); cpu_baseline_per_config times BASELINE
+               configs 1, 3, 4 (16-token subset, extrapolated), 5a and 5b the
+               same way, with the host CPU model and core count.
+Every extra whose working set could sit in the 256 MB Infinity Cache
+rotates distinct copies totalling more than 512 MB.
 """
 from __future__ import annotations
 
@@ -78,6 +87,24 @@ def measured_traffic():
     except OSError:
         pass
     return None, None
+
+
+def host_cpu() -> dict:
+    """The host CPU model and the cores this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count()
+    return {"model": model, "nproc": nproc, "os_cpu_count": os.cpu_count()}
 
 
 def parse():
@@ -312,7 +339,39 @@ def main() -> int:
     b = qbytes(HIDDEN, FFN) + 2 * FFN + 4 * HIDDEN
     kernels["down_add_2048x11008"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
 
-    extras = {}
+    # ------------------------------------------------ launch / stream floors
+    # An empty kernel per graph launch, and a pure 16-byte streaming read of
+    # each decode projection's bytes from 36 distinct buffers (more than the
+    # Infinity Cache holds): what any kernel of that size can reach here.
+    import ctypes
+    flib = ctypes.CDLL(os.path.join(ROOT, "reflex-infer_amd", "lib", "librxq4_floors.so"))
+    flib.rxq4_floor_empty.argtypes = [ctypes.c_void_p]
+    flib.rxq4_floor_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_void_p]
+    floors = {}
+    med, _ = per_launch(lambda i: flib.rxq4_floor_empty(sp), R)
+    floors["empty_kernel_us"] = round(med, 3)
+    for name, nbytes in (("o_2048x2048", qbytes(HIDDEN, HIDDEN)),
+                         ("qkv_2560x2048", qbytes(sum(QKV), HIDDEN)),
+                         ("down_2048x11008", qbytes(HIDDEN, FFN)),
+                         ("gate_up_22016x2048", qbytes(2 * FFN, HIDDEN))):
+        nb16 = (nbytes + 15) // 16 * 16
+        bufs = [torch.empty(nb16, dtype=torch.uint8, device=dev) for _ in range(36)]
+        sink = torch.empty(nb16 // 16 // 256 + 1, dtype=torch.int32, device=dev)
+        best = None
+        for u in (1, 2, 4, 8):  # loads per thread; the fastest is the floor
+            med, _ = per_launch(lambda i: flib.rxq4_floor_read(bufs[i % 36].data_ptr(), nb16,
+                                                               sink.data_ptr(), u, sp), R)
+            if best is None or med < best[0]:
+                best = (med, u)
+        floors[f"stream_read_{name}"] = {"bytes": nb16, "us": round(best[0], 3),
+                                         "GBps": round(nb16 / best[0] / 1e3, 1),
+                                         "loads_per_thread": best[1]}
+        del bufs, sink
+    log(f"floors: {floors}")
+
+    extras = {"floors": floors}
+    table_host = ids_np = uniq = None
     if not args.no_extras:
         # LM head: three tables in rotation, so a table is read again only
         # after 350 MB of others have passed the 256 MB Infinity Cache.
@@ -340,6 +399,7 @@ def main() -> int:
             capi.embed_rows_f16(emb, heads[i % 3], VOCAB, ids, HIDDEN, stream=sp)
         med, _ = per_launch(emb_launch, 20)
         uniq = int(np.unique(ids_np).size)
+        table_host = heads[0].cpu().numpy() if not args.no_cpu_baseline else None
         b = uniq * qbytes(1, HIDDEN) + 4096 * HIDDEN * 2 + 4096 * 4
         kernels["embed_gather_4096_zipf"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1),
                                              "unique_rows": uniq}
@@ -352,26 +412,26 @@ def main() -> int:
             return qweights(seed, rows, K, ggml_type=14)
 
         q6b = lambda rows, K: rows * (K // 256) * 210  # noqa: E731
-        heads6 = [q6_blocks(60_000 + i, VOCAB, HIDDEN) for i in range(2)]
+        heads6 = [q6_blocks(60_000 + i, VOCAB, HIDDEN) for i in range(3)]  # 574 MB
 
         def lm6_launch(i):
-            capi.gemv_f32(logits, heads6[i % 2], x_h, VOCAB, HIDDEN, stream=sp, ggml_type=14)
-        med, _ = per_launch(lm6_launch, 20)
+            capi.gemv_f32(logits, heads6[i % 3], x_h, VOCAB, HIDDEN, stream=sp, ggml_type=14)
+        med, _ = per_launch(lm6_launch, 21)
         b = q6b(VOCAB, HIDDEN) + 2 * HIDDEN + 4 * VOCAB
         kernels["q6k_lm_head_f32_151936x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
 
         def emb6_launch(i):
-            capi.embed_rows_f16(emb, heads6[i % 2], VOCAB, ids, HIDDEN, stream=sp, ggml_type=14)
-        med, _ = per_launch(emb6_launch, 20)
+            capi.embed_rows_f16(emb, heads6[i % 3], VOCAB, ids, HIDDEN, stream=sp, ggml_type=14)
+        med, _ = per_launch(emb6_launch, 21)
         b = uniq * q6b(1, HIDDEN) + 4096 * HIDDEN * 2 + 4096 * 4
         kernels["q6k_embed_gather_4096_zipf"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
         del heads6
 
-        downs6 = [q6_blocks(61_000 + i, HIDDEN, FFN) for i in range(8)]
+        downs6 = [q6_blocks(61_000 + i, HIDDEN, FFN) for i in range(36)]  # 558 MB
 
         def d6_launch(i):
-            capi.gemv_add_f16(y_d, downs6[i % 8], x_f, res, HIDDEN, FFN, stream=sp, ggml_type=14)
-        med, _ = per_launch(d6_launch, 40)
+            capi.gemv_add_f16(y_d, downs6[i % 36], x_f, res, HIDDEN, FFN, stream=sp, ggml_type=14)
+        med, _ = per_launch(d6_launch, 72)
         b = q6b(HIDDEN, FFN) + 2 * FFN + 4 * HIDDEN
         kernels["q6k_down_add_2048x11008"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
         del downs6
@@ -391,34 +451,36 @@ def main() -> int:
         # Attention (decode at 4096 positions, prefill of 512 tokens) with
         # Qwen3-4B-like heads: 32 query heads, 8 KV heads, head_dim 128.
         AH, AKV, AD = 32, 8, 128
+        # 36 K/V pairs of 16.8 MB (604 MB)
         caches = [(gen(70_000 + i, (4096, AKV, AD), 1.0).half(), gen(71_000 + i, (4096, AKV, AD), 1.0).half())
-                  for i in range(4)]
+                  for i in range(36)]
         qa = gen(72_000, (AH * AD,), 1.0).half()
         oa = torch.empty(AH * AD, dtype=torch.float16, device=dev)
 
         def attn_launch(i):
-            k, v = caches[i % 4]
+            k, v = caches[i % 36]
             capi.attention_decode_f16(oa, qa, k, v, AH, AKV, AD, 4096, AD ** -0.5, stream=sp)
-        med, _ = per_launch(attn_launch, 40)
+        med, _ = per_launch(attn_launch, 72)
         b = 2 * 4096 * AKV * AD * 2
         kernels["attn_decode_fp16_4096"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
         qp = gen(73_000, (512, AH * AD), 1.0).half()
         op = torch.empty_like(qp)
 
         def prefill_launch(i):
-            k, v = caches[i % 4]
+            k, v = caches[i % 36]
             capi.attention_prefill_f16(op, qp, k, v, AH, AKV, AD, 512, 0, AD ** -0.5, stream=sp)
         med, _ = per_launch(prefill_launch, 8)
         fl = 4.0 * AH * AD * sum(t + 1 for t in range(512))
         kernels["attn_prefill_fp16_512"] = {"us": round(med, 3), "TFLOPs": round(fl / med / 1e6, 2)}
         del caches
+        # 9 K/V pairs of 67 MB (604 MB)
         long_kv = [(gen(74_000 + i, (16384, AKV, AD), 1.0).half(), gen(75_000 + i, (16384, AKV, AD), 1.0).half())
-                   for i in range(2)]
+                   for i in range(9)]
 
         def attn_long(i):
-            k, v = long_kv[i % 2]
+            k, v = long_kv[i % 9]
             capi.attention_decode_f16(oa, qa, k, v, AH, AKV, AD, 16384, AD ** -0.5, stream=sp)
-        med, _ = per_launch(attn_long, 20)
+        med, _ = per_launch(attn_long, 36)
         b = 2 * 16384 * AKV * AD * 2
         kernels["attn_decode_fp16_16384"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
         del long_kv
@@ -443,14 +505,14 @@ def main() -> int:
         # Prefill GEMM at m = 512 and 2048 (bf16
         # activations, bf16 out).
         for (M, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):
-            ws = [qweights(30_000 + M + i, M, K) for i in range(4)]
+            ws = [qweights(30_000 + M + i, M, K) for i in range(42)]  # 533 MB
             for m in (512, 2048):
                 xb = gen(40_000 + K + m, (m, K), 1.0).to(torch.bfloat16)
                 yb = torch.empty((m, M), dtype=torch.bfloat16, device=dev)
 
                 def gm_launch(i, xb=xb, yb=yb, m=m):
-                    capi.gemm(yb, ws[i % 4], xb, M, m, K, stream=sp)
-                med, _ = per_launch(gm_launch, 20 if m == 512 else 8)
+                    capi.gemm(yb, ws[i % 42], xb, M, m, K, stream=sp)
+                med, _ = per_launch(gm_launch, 42 if m == 512 else 21)
                 tf = 2 * m * M * K / med / 1e6
                 kernels[f"gemm_bf16_m{m}_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1),
                                                       "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
@@ -462,37 +524,91 @@ def main() -> int:
         # some FFN and V tensors in these formats).
         for t, tname in ((14, "q6k"), (13, "q5k")):
             for (M, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):
-                ws = [qweights(31_000 + M + i, M, K, ggml_type=t) for i in range(2)]
+                ws = [qweights(31_000 + M + i, M, K, ggml_type=t) for i in range(36)]
                 xb = gen(41_000 + K, (512, K), 1.0).to(torch.bfloat16)
                 yb = torch.empty((512, M), dtype=torch.bfloat16, device=dev)
 
                 def kq_launch(i, ws=ws, xb=xb, yb=yb, M=M, K=K, t=t):
-                    capi.gemm(yb, ws[i % 2], xb, M, 512, K, stream=sp, ggml_type=t)
-                med, _ = per_launch(kq_launch, 6)
+                    capi.gemm(yb, ws[i % 36], xb, M, 512, K, stream=sp, ggml_type=t)
+                med, _ = per_launch(kq_launch, 36)
                 tf = 2 * 512 * M * K / med / 1e6
                 kernels[f"{tname}_gemm_bf16_m512_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1)}
                 del ws
 
     # ------------------------------------------------------- CPU baseline
     cpu = None
+    cpu_cfg = None
     if not args.no_cpu_baseline:
         from oracle import oracle as orc
-        log("CPU baseline: oracle restatement of gemv_quant_cpu over 36 layers, 1 thread")
+        log("CPU baseline: oracle restatement of gemv_quant_cpu, 1 thread, median of 5")
         xs = {HIDDEN: x_h.cpu().numpy().view(np.uint16), FFN: x_f.cpu().numpy().view(np.uint16)}
         hostw = [{k: v.cpu().numpy() for k, v in L.items()} for L in layers]
-        t0 = time.perf_counter()
-        for L in hostw:
-            orc.gemv_f32(L["qkv"], HIDDEN, xs[HIDDEN])
-            orc.gemv_f32(L["o"], HIDDEN, xs[HIDDEN])
-            orc.gemv_f32(L["gu"], HIDDEN, xs[HIDDEN])
-            orc.gemv_f32(L["down"], FFN, xs[FFN])
-        cpu_s = time.perf_counter() - t0
+
+        def median_s(fn, runs=5):
+            t = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                fn()
+                t.append(time.perf_counter() - t0)
+            return float(np.median(t))
+
+        def step_cpu():
+            for L in hostw:
+                orc.gemv_f32(L["qkv"], HIDDEN, xs[HIDDEN])
+                orc.gemv_f32(L["o"], HIDDEN, xs[HIDDEN])
+                orc.gemv_f32(L["gu"], HIDDEN, xs[HIDDEN])
+                orc.gemv_f32(L["down"], FFN, xs[FFN])
+        cpu_s = median_s(step_cpu)
+        host = host_cpu()
         cpu = {"value": round(step_bytes / cpu_s / 1e9, 3), "unit": "GB/s", "cores": 1,
                "kind": "port",
-               "sample": "full 36-layer decode set (one step), fp32 outputs, single thread; "
-                         f"{cpu_s:.2f} s",
+               "sample": "full 36-layer decode set (one step), fp32 outputs, single thread, "
+                         f"median of 5: {cpu_s:.3f} s; host {host['model']}, "
+                         f"{host['nproc']} cores visible",
                "ms_per_step": round(cpu_s * 1e3, 1)}
         log(f"CPU baseline {cpu['value']} GB/s ({cpu_s:.2f} s per step)")
+        cpu_cfg = {"host": host, "threads": 1, "runs": 5, "statistic": "median",
+                   "kind": "port (oracle/q4k_oracle.c, the reference gemv_quant_cpu loop)"}
+        # W[2048 x 2048], x fp32 -> fp16, y fp32
+        w1 = hostw[0]["o"]
+        t = median_s(lambda: orc.gemv_f32(w1, HIDDEN, xs[HIDDEN]))
+        b = qbytes(HIDDEN, HIDDEN) + 2 * HIDDEN + 4 * HIDDEN
+        cpu_cfg["cfg1_gemv_2048x2048"] = {"us": round(t * 1e6, 1), "GBps": round(b / t / 1e9, 3)}
+        # m independent GEMVs (the reference's batched host path
+        # is per-token GEMV, q4_gemm.cu:1735-1739)
+        cfg3 = {}
+        for name, key, M, K in (("gate_up", "gu", 2 * FFN, HIDDEN), ("down", "down", HIDDEN, FFN)):
+            W = hostw[0][key]
+            for m in (1, 2, 4, 8, 16):
+                xm = np.random.default_rng(60 + m).standard_normal((m, K)).astype(np.float16).view(np.uint16)
+                t = median_s(lambda: orc.gemm_tokens_f32(W, K, xm))
+                b = qbytes(M, K) + m * K * 2 + m * M * 2
+                cfg3[f"{name}_{M}x{K}_m{m}"] = {"us": round(t * 1e6, 1), "GBps": round(b / t / 1e9, 3)}
+        cpu_cfg["cfg3_small_batch"] = cfg3
+        # a 16-token subset, extrapolated linearly to m tokens
+        cfg4 = {}
+        for M, K, key in ((FFN, HIDDEN, None), (HIDDEN, FFN, "down")):
+            W = hostw[0]["down"] if key else hostw[0]["gu"][:FFN]
+            x16 = np.random.default_rng(70).standard_normal((16, K)).astype(np.float16).view(np.uint16)
+            t16 = median_s(lambda: orc.gemm_tokens_f32(W, K, x16))
+            for m in (512, 2048):
+                t = t16 * m / 16
+                cfg4[f"gemm_m{m}_{M}x{K}"] = {"us": round(t * 1e6, 1),
+                                              "GFLOPs": round(2 * m * M * K / t / 1e9, 3),
+                                              "measured_tokens": 16, "extrapolated": True}
+        cpu_cfg["cfg4_prefill_gemm"] = cfg4
+        # embedding gather (restated row dequant; the reference
+        # has no CPU embedding path) and the LM head GEMV, full size
+        if table_host is not None:
+            t = median_s(lambda: orc.embed_rows_f16(table_host, HIDDEN, ids_np))
+            b = uniq * qbytes(1, HIDDEN) + 4096 * HIDDEN * 2 + 4096 * 4
+            cpu_cfg["cfg5a_embed_gather_4096"] = {"us": round(t * 1e6, 1),
+                                                  "GBps": round(b / t / 1e9, 3)}
+            t = median_s(lambda: orc.gemv_f32(table_host, HIDDEN, xs[HIDDEN]))
+            b = qbytes(VOCAB, HIDDEN) + 2 * HIDDEN + 4 * VOCAB
+            cpu_cfg["cfg5b_lm_head_151936x2048"] = {"us": round(t * 1e6, 1),
+                                                    "GBps": round(b / t / 1e9, 3)}
+        log(f"CPU per-config baseline done ({host['model']})")
 
     out = {
         "metric": METRIC,
@@ -519,6 +635,7 @@ def main() -> int:
         "eager_ms_per_step": round(eager_ms, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_per_config": cpu_cfg,
         "per_kernel": kernels,
     }
     out.update(extras)

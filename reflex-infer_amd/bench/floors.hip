@@ -1,0 +1,66 @@
+// floors.hip -- measurement kernels for bench.py (not part of the drop-in
+// library): what a launch and a pure stream of the same bytes cost on the
+// box, the floors against which the GEMV kernels are judged.
+//   rxq4_floor_empty(stream)                       an empty kernel (one wave)
+//   rxq4_floor_read(src, bytes, sink, u, stream)    reads `bytes` (a multiple
+//       of 16) once: thread t issues u (1, 2, 4 or 8) 16-byte loads, at
+//       t and t + threads, t + 2 threads, ... (coalesced per load), all
+//       before any use; one dword per workgroup goes to `sink` so the loads
+//       stay live.  bench.py takes the fastest u.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void floor_empty_kernel() {}
+
+template <int U>
+__global__ __launch_bounds__(256) void floor_read_kernel(const u32x4 *__restrict__ src,
+                                                         int64_t n16, uint32_t *sink) {
+    const int64_t threads = (int64_t)gridDim.x * 256;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    u32x4 v[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t i = t + j * threads;
+        v[j] = i < n16 ? src[i] : u32x4{0, 0, 0, 0};
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < U; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    __shared__ uint32_t red[256];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t s = 0;
+        for (int i = 0; i < 256; ++i) s ^= red[i];
+        sink[blockIdx.x] = s;
+    }
+}
+
+extern "C" {
+
+int rxq4_floor_empty(void *stream) {
+    floor_empty_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>();
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// sink: at least ceil(bytes / 16 / u / 256) dwords
+int rxq4_floor_read(const void *src, int64_t bytes, uint32_t *sink, int u, void *stream) {
+    if (bytes <= 0 || bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(src) & 15) != 0) return 4;
+    const int64_t n16 = bytes / 16;
+    const int64_t threads = (n16 + u - 1) / u;
+    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const u32x4 *s = static_cast<const u32x4 *>(src);
+    switch (u) {
+        case 1: floor_read_kernel<1><<<blocks, 256, 0, st>>>(s, n16, sink); break;
+        case 2: floor_read_kernel<2><<<blocks, 256, 0, st>>>(s, n16, sink); break;
+        case 4: floor_read_kernel<4><<<blocks, 256, 0, st>>>(s, n16, sink); break;
+        case 8: floor_read_kernel<8><<<blocks, 256, 0, st>>>(s, n16, sink); break;
+        default: return 4;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+}  // extern "C"

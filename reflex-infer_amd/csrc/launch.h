@@ -22,9 +22,9 @@ struct Scratch {
     size_t bytes = 0;
     size_t capacity() const { return ptr ? bytes : kWorkspaceBytes; }
     // `need` bytes of it; launchers size their splits to fit, so a request
-    // beyond the capacity is a launcher bug and fails without a launch
+    // beyond the capacity is refused (no launch) rather than overrun
     hipError_t get(hipStream_t st, size_t need, float **p) const {
-        if (need > capacity()) return hipErrorInvalidValue;
+        if (need > capacity()) return hipErrorOutOfMemory;
         if (ptr) {
             *p = ptr;
             return hipSuccess;

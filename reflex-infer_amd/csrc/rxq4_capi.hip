@@ -44,6 +44,10 @@ int ok() { return rxq4::set_ok(); }
 
 int from_hip(hipError_t e, const char *what) {
     if (e == hipSuccess) return ok();
+    if (e == hipErrorOutOfMemory)  // rxq4::Scratch::get, or the workspace allocation
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT,
+                         "%s: the fp32 split partials do not fit the scratch / workspace (%s)",
+                         what, hipGetErrorString(e));
     return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: HIP error %s", what, hipGetErrorString(e));
 }
 

@@ -20,6 +20,7 @@ from tests import util
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.host_path
 def test_upload_bytes_and_gemv_through_alias(tmp_path):
     K = 2048
     q4 = util.weights(850, 256, K)
@@ -45,9 +46,12 @@ def test_upload_bytes_and_gemv_through_alias(tmp_path):
         ref = orc.gemv_f32(f.host_array(t.name), K, x16)
         got = y.view(torch.int16).cpu().numpy().view(np.uint16)
         assert util.rounded_ok(got, ref).all()
-        # Host-only weights (no alias) are refused: there is no CPU fallback.
+        # The mapped host address alone (no alias) takes the reference's host
+        # path (q4_gemm.cu:1886-1899): bit for bit its CPU loop.
         a.weights_device = None
-        assert api.call("gemv_quant", a) == rxq4.INVALID_ARGUMENT
+        assert api.call("gemv_quant", a) == rxq4.SUCCESS
+        got = y.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got, orc.gemv_f16(f.host_array(t.name), K, x16))
         # Q6_K embedding row through the alias, bit-exact.
         e = f.tensors["token_embd.weight"]
         dst = torch.empty(K, dtype=torch.float16, device="cuda")
