@@ -111,6 +111,22 @@ int rxq4_embed_row_f16(void *dst, const void *w, int ggml_type, int token_id,
 int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
               int x_dtype, int M, int N, int K, void *stream);
 
+/* NEW.  rxq4_gemm with no allocation: same arguments, routing, kernels and
+ * results, but the fp32 partials of its split launches live in a fixed
+ * 48 MiB device array of the library (one per device, made by the HIP
+ * runtime when the entry point is first called on that device and held
+ * until the process ends) instead of the stream's workspace, so no call ever allocates device
+ * memory (no hipMalloc/hipFree/allocating library call).  No counterpart in
+ * the reference; it is for callers that cannot allocate: code under HIP graph
+ * capture, serving loops, harnesses that forbid allocation.  The split counts
+ * are sized so the partials fit the array; a plan needing more is refused
+ * (InvalidArgument, nothing launched).  The array keeps the last call's
+ * contents and every call on a device shares it: calls that overlap on one
+ * device (two streams, or two threads) race and must be serialised by the
+ * caller. */
+int rxq4_gemm_noalloc(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
+                      int x_dtype, int M, int N, int K, void *stream);
+
 /* NEW.  Batched gather: dst[i, :] fp16 = dequant(W[ids[i], :]) for i < n_ids.
  * ids is a device int32 array; ids outside [0, n_vocab) give a zero row. */
 int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab,

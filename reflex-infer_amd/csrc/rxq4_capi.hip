@@ -8,6 +8,8 @@
 #include "rxq4.h"
 
 #include <stdarg.h>
+
+#include <atomic>
 #include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
@@ -232,6 +234,52 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
               int M, int N, int K, void *stream) {
     return gemm_impl("rxq4_gemm", y, y_dtype, w, ggml_type, x, x_dtype, M, N, K, stream,
                      rxq4::Scratch{});
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------ rxq4_gemm_noalloc
+// The split partials of rxq4_gemm_noalloc live in this file-scope array:
+// each device holds its own copy (kNoAllocScratchBytes), made when the HIP
+// runtime loads this file's code object on it (at the first
+// hipGetSymbolAddress below) and held until the process ends.  Host code
+// never uses the array's name as an address: the device address is taken
+// once per device with hipGetSymbolAddress and kept in g_scratch_addr.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = rxq4::kWorkspaceBytes;  // 48 MiB
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+std::atomic<float *> g_scratch_addr[kMaxDevices];
+
+hipError_t scratch_address(float **p) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    float *a = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (!a) {
+        void *q = nullptr;
+        if ((e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        a = static_cast<float *>(q);
+        g_scratch_addr[dev].store(a, std::memory_order_release);
+    }
+    *p = a;
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rxq4_gemm_noalloc(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
+                      int x_dtype, int M, int N, int K, void *stream) {
+    const char *fn = "rxq4_gemm_noalloc";
+    float *sp = nullptr;
+    const hipError_t e = scratch_address(&sp);
+    if (e != hipSuccess) return from_hip(e, fn);
+    return gemm_impl(fn, y, y_dtype, w, ggml_type, x, x_dtype, M, N, K, stream,
+                     rxq4::Scratch{sp, kNoAllocScratchBytes});
 }
 
 int rxq4_gemm_f16(void *y, const void *w, int ggml_type, const void *x, int M, int N, int K,

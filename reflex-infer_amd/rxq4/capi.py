@@ -34,6 +34,8 @@ SIGNATURES = {
                           c_int, c_void_p]),
     "rxq4_embed_rows_f16": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int, c_int,
                                     c_void_p]),
+    "rxq4_gemm_noalloc": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
+                                  c_int, c_void_p]),
     "rxq4_quantize_q4k": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p]),
     "rxq4_quantize": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p]),
     "rxq4_attention_decode_f16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
@@ -130,6 +132,14 @@ def gemm(y, w, x, M, N, K, stream=None, ggml_type=GGML_TYPE_Q4_K):
     """Typed GEMM: dtypes taken from the tensors (x fp16|bf16, y fp32|fp16|bf16)."""
     return _check(lib().rxq4_gemm(_ptr(y), _dtype_code(y), _ptr(w), ggml_type, _ptr(x),
                                   _dtype_code(x), M, N, K, _stream(stream)), "rxq4_gemm")
+
+
+def gemm_noalloc(y, w, x, M, N, K, stream=None, ggml_type=GGML_TYPE_Q4_K):
+    """rxq4_gemm with its split partials in the library's fixed device array
+    (allocates nothing)."""
+    return _check(lib().rxq4_gemm_noalloc(_ptr(y), _dtype_code(y), _ptr(w), ggml_type, _ptr(x),
+                                          _dtype_code(x), M, N, K, _stream(stream)),
+                  "rxq4_gemm_noalloc")
 
 
 def embed_row_f16(dst, w, token_id, hidden, stream=None, ggml_type=GGML_TYPE_Q4_K):
