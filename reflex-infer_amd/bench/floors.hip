@@ -2,11 +2,12 @@
 // library): what a launch and a pure stream of the same bytes cost on the
 // box, the floors against which the GEMV kernels are judged.
 //   rxq4_floor_empty(stream)                       an empty kernel (one wave)
-//   rxq4_floor_read(src, bytes, sink, u, stream)    reads `bytes` (a multiple
-//       of 16) once: thread t issues u (1, 2, 4 or 8) 16-byte loads, at
-//       t and t + threads, t + 2 threads, ... (coalesced per load), all
-//       before any use; one dword per workgroup goes to `sink` so the loads
-//       stay live.  bench.py takes the fastest u.
+//   rxq4_floor_read(src, bytes, sink, blocks, stream)    reads `bytes` (a
+//       multiple of 16) once with `blocks` workgroups of 256 threads: thread
+//       t issues its u = ceil(bytes / 16 / threads) 16-byte loads (at t,
+//       t + threads, ..., coalesced per load; u <= 16) before any use; one
+//       dword per workgroup goes to `sink` so the loads stay live.  bench.py
+//       takes the fastest of a few grid sizes.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -45,21 +46,20 @@ int rxq4_floor_empty(void *stream) {
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
-// sink: at least ceil(bytes / 16 / u / 256) dwords
-int rxq4_floor_read(const void *src, int64_t bytes, uint32_t *sink, int u, void *stream) {
+// sink: at least `blocks` dwords
+int rxq4_floor_read(const void *src, int64_t bytes, uint32_t *sink, int blocks, void *stream) {
     if (bytes <= 0 || bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(src) & 15) != 0) return 4;
+    if (blocks <= 0) return 4;
     const int64_t n16 = bytes / 16;
-    const int64_t threads = (n16 + u - 1) / u;
-    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    const int64_t u = (n16 + (int64_t)blocks * 256 - 1) / ((int64_t)blocks * 256);
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const u32x4 *s = static_cast<const u32x4 *>(src);
-    switch (u) {
-        case 1: floor_read_kernel<1><<<blocks, 256, 0, st>>>(s, n16, sink); break;
-        case 2: floor_read_kernel<2><<<blocks, 256, 0, st>>>(s, n16, sink); break;
-        case 4: floor_read_kernel<4><<<blocks, 256, 0, st>>>(s, n16, sink); break;
-        case 8: floor_read_kernel<8><<<blocks, 256, 0, st>>>(s, n16, sink); break;
-        default: return 4;
-    }
+    if (u <= 1) floor_read_kernel<1><<<blocks, 256, 0, st>>>(s, n16, sink);
+    else if (u <= 2) floor_read_kernel<2><<<blocks, 256, 0, st>>>(s, n16, sink);
+    else if (u <= 4) floor_read_kernel<4><<<blocks, 256, 0, st>>>(s, n16, sink);
+    else if (u <= 8) floor_read_kernel<8><<<blocks, 256, 0, st>>>(s, n16, sink);
+    else if (u <= 16) floor_read_kernel<16><<<blocks, 256, 0, st>>>(s, n16, sink);
+    else return 4;
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
