@@ -107,6 +107,72 @@ def host_cpu() -> dict:
     return {"model": model, "nproc": nproc, "os_cpu_count": os.cpu_count()}
 
 
+# Single-kernel workloads for counter collection (bench.py --leg NAME):
+# (ggml type, rows, K, tokens, kind); weights are distinct copies so that
+# every launch streams from HBM.
+LEGS = {
+    "gate_up": (12, 2 * FFN, HIDDEN, 1, "pair"),
+    "down": (12, HIDDEN, FFN, 1, "add"),
+    "lm_head": (12, VOCAB, HIDDEN, 1, "f32"),
+    "embed": (12, VOCAB, HIDDEN, 4096, "embed"),
+    "gemm512_11008x2048": (12, FFN, HIDDEN, 512, "gemm"),
+    "gemm512_2048x11008": (12, HIDDEN, FFN, 512, "gemm"),
+}
+
+
+def run_leg(name: str) -> int:
+    import numpy as np
+    import torch
+
+    import rxq4
+    from rxq4 import capi
+
+    rxq4.load()
+    dev = torch.device("cuda:0")
+    t, M, K, m, kind = LEGS[name]
+    n_copies = 3 if M == VOCAB else max(2, -(-(600 << 20) // qbytes(M, K)))
+
+    def gen(seed, shape, sigma):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        return torch.randn(shape, generator=g, device=dev) * sigma
+
+    ws = [capi.quantize_ggml(gen(80_000 + i, (M, K), 0.02), t) for i in range(n_copies)]
+    launches = 20
+    if kind == "embed":
+        rng = np.random.default_rng(5)
+        ranks = np.arange(1, VOCAB + 1, dtype=np.float64)
+        cdf = np.cumsum(ranks ** -1.1)
+        cdf /= cdf[-1]
+        ids = torch.from_numpy(rng.permutation(VOCAB)[np.minimum(
+            np.searchsorted(cdf, rng.random(m)), VOCAB - 1)].astype(np.int32)).to(dev)
+        out = torch.empty((m, K), dtype=torch.float16, device=dev)
+        run = lambda i: capi.embed_rows_f16(out, ws[i % n_copies], VOCAB, ids, K)  # noqa: E731
+    elif kind == "gemm":
+        xb = gen(1, (m, K), 1.0).to(torch.bfloat16)
+        yb = torch.empty((m, M), dtype=torch.bfloat16, device=dev)
+        run = lambda i: capi.gemm(yb, ws[i % n_copies], xb, M, m, K)  # noqa: E731
+    else:
+        x = gen(2, (K,), 1.0).half()
+        if kind == "f32":
+            y = torch.empty(M, dtype=torch.float32, device=dev)
+            run = lambda i: capi.gemv_f32(y, ws[i % n_copies], x, M, K)  # noqa: E731
+        elif kind == "add":
+            y = torch.empty(M, dtype=torch.float16, device=dev)
+            res = gen(3, (M,), 1.0).half()
+            run = lambda i: capi.gemv_add_f16(y, ws[i % n_copies], x, res, M, K)  # noqa: E731
+        else:
+            y = torch.empty(M, dtype=torch.float16, device=dev)
+            h = M // 2
+            run = lambda i: capi.gemv_multi_f16(  # noqa: E731
+                [(y[:h], ws[i % n_copies][:h], h), (y[h:], ws[i % n_copies][h:], h)], x, K)
+    torch.cuda.synchronize()
+    for i in range(launches):
+        run(i)
+    torch.cuda.synchronize()
+    print(json.dumps({"leg": name, "launches": launches, "weight_copies": n_copies}), flush=True)
+    return 0
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -117,11 +183,16 @@ def parse():
     ap.add_argument("--eager", action="store_true", help="time eager launches, not a graph")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (PMC byte-counter calibration)")
+    ap.add_argument("--leg", choices=sorted(LEGS),
+                    help="only run one kernel's workload, eagerly, 20 launches on distinct "
+                         "weights (for rocprofv3 counter passes); prints one JSON line")
     return ap.parse_args()
 
 
 def main() -> int:
     args = parse()
+    if args.leg:
+        return run_leg(args.leg)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the Q4_K kernels run on one MI355X; sharding is design-only). "

@@ -19,61 +19,12 @@
 #include <mutex>
 
 #include "launch.h"
+#include "gemm_util.h"
 #include "mfma_util.h"
 #include "q4k_device.h"
 #include "rxq4.h"
 
 namespace rxq4 {
-
-// Two fp32 values from bytes 2*word, 2*word+1 of m.  Each byte is a nibble
-// value q in [0, 15]; read as an FP8 E4M3 (OCP) pattern it is exactly
-// q * 2^-9 (subnormal for q < 8), so v_cvt_pk_f32_fp8 turns two nibbles
-// into exact floats with one instruction.
-template <bool WORD>
-__device__ __forceinline__ f32x2 nibbles_f32(uint32_t m) {
-    return __builtin_amdgcn_cvt_pk_f32_fp8((int)m, WORD);
-}
-
-// Four weights from the four nibble bytes of m: w = scale512 * (q * 2^-9)
-// - dm with scale512 = d*sc*512, i.e. d*sc*q - dmin*m with the single fp32
-// rounding of the reference (the product is exact), then RNE to the operand
-// type.
-template <int XT>
-__device__ __forceinline__ void dequant4(uint32_t m, float scale512, float dm, uint32_t *out) {
-    const f32x2 f01 = nibbles_f32<false>(m), f23 = nibbles_f32<true>(m);
-    out[0] = pack2<XT>(scale512 * f01[0] - dm, scale512 * f01[1] - dm);
-    out[1] = pack2<XT>(scale512 * f23[0] - dm, scale512 * f23[1] - dm);
-}
-
-// Nibble bytes of v: low nibbles (hi = false) or high nibbles.
-__device__ __forceinline__ uint32_t nibble_bytes(uint32_t v, bool hi) {
-    return (hi ? (v >> 4) : v) & 0x0F0F0F0Fu;
-}
-
-// Eight weights from the low (hi = false) or high nibbles of bytes v0, v1.
-template <int XT>
-__device__ __forceinline__ u32x4 dequant8(uint32_t v0, uint32_t v1, bool hi, float scale512,
-                                          float dm) {
-    uint32_t o[4];
-    dequant4<XT>(nibble_bytes(v0, hi), scale512, dm, o);
-    dequant4<XT>(nibble_bytes(v1, hi), scale512, dm, o + 2);
-    return u32x4{o[0], o[1], o[2], o[3]};
-}
-
-// Scales of one weight row for quant group il: sub-block 2il (low nibbles)
-// and 2il+1 (high nibbles), each times 512 for dequant4.
-struct GroupScales {
-    float lo, hi, dm_lo, dm_hi;
-};
-
-__device__ __forceinline__ GroupScales group_scales(u32x4 h, int il) {
-    const float d = f16_bits_to_f32(h.x & 0xFFFFu), dmin = f16_bits_to_f32(h.x >> 16);
-    uint32_t sc, mn;
-    scale_pair(h.y, h.z, h.w, il, &sc, &mn);
-    const float d512 = d * 512.0f;
-    return GroupScales{d512 * (float)(sc & 0xFFu), d512 * (float)(sc >> 8),
-                       dmin * (float)(mn & 0xFFu), dmin * (float)(mn >> 8)};
-}
 
 // ---------------------------------------------------------------------------
 // Tiled GEMM.
@@ -137,39 +88,6 @@ struct GemmParams {
     int total_units, units_per_xcd;
 };
 
-template <int YT>
-__device__ __forceinline__ void store4(void *y, int64_t idx, f32x4 v, bool vec_ok, int valid) {
-    if (vec_ok) {
-        if (YT == RXQ4_DTYPE_F32) {
-            *reinterpret_cast<f32x4 *>(static_cast<float *>(y) + idx) = v;
-        } else {
-            uint32_t lo, hi;
-            if (YT == RXQ4_DTYPE_F16) {
-                lo = f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
-                hi = f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
-            } else {
-                lo = f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
-                hi = f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
-            }
-            *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(y) + idx) = u32x2{lo, hi};
-        }
-    } else {
-        for (int r = 0; r < valid; ++r) store_out<YT>(y, idx + r, v[r]);
-    }
-}
-
-// 32x32x16 MFMA (fp32 accumulate) with operands of the x type.  Lane l:
-// src0 = row l%32, 8 k values in slot 8*(l/32); src1 = token l%32, same k
-// slot; dst element i = row 8*(i/4) + 4*(l/32) + i%4 of token l%32.
-template <int XT>
-__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-    if (XT == RXQ4_DTYPE_BF16)
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
 constexpr int kW8Rows = 32;                       // weight rows per wave
 constexpr int kOutPitch = kRowsPerWg * 2 + 16;    // staged output: bytes per token
 
@@ -202,10 +120,11 @@ struct GemmFmt<12> {
         const uint8_t *row;  // the lane's row at the first super-block
         int nsb, h;
         // super-block indices clamp to the last one: loads past the end stay in the row
+        __device__ int blk(int sb) const { return min(sb, nsb - 1); }
         __device__ Stage stage(int sb, int g) const {
-            return {load16(row + min(sb, nsb - 1) * kBytes + 16 + 32 * g + 16 * h)};
+            return {load16(row + blk(sb) * kBytes + 16 + 32 * g + 16 * h)};
         }
-        __device__ Sb header(int sb) const { return {load16(row + min(sb, nsb - 1) * kBytes)}; }
+        __device__ Sb header(int sb) const { return {load16(row + blk(sb) * kBytes)}; }
     };
     using Scales = GroupScales;
     __device__ static Scales scales(const Sb &b, int g) { return group_scales(b.h, g); }
@@ -252,11 +171,12 @@ struct GemmFmt<13> {
     struct Loader {
         const uint8_t *row;
         int nsb, h;
+        __device__ int blk(int sb) const { return min(sb, nsb - 1); }
         __device__ Stage stage(int sb, int g) const {
-            return {load16(row + min(sb, nsb - 1) * kBytes + 48 + 32 * g + 16 * h)};
+            return {load16(row + blk(sb) * kBytes + 48 + 32 * g + 16 * h)};
         }
         __device__ Sb header(int sb) const {
-            const uint8_t *b = row + min(sb, nsb - 1) * kBytes;
+            const uint8_t *b = row + blk(sb) * kBytes;
             return {load16(b), load16(b + 16 + 16 * h)};
         }
     };
@@ -396,12 +316,13 @@ struct GemmFmt<14> {
     }
 };
 
-template <int T, int XT, int YT>
+template <int T, int XT, int YT, int TM>
 __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     using F = GemmFmt<T>;
-    constexpr int TM = 128;          // tokens per workgroup tile
-    constexpr int NT = TM / 32;      // 32-token fragments
-    constexpr int kXLoads = 2;       // 1 KB direct-to-LDS copies per wave per stage
+    // TM tokens per workgroup tile (128 or 256)
+    constexpr int NT = TM / 32;      // 32-token fragments per wave
+    constexpr int MPS = 4 * NT;      // MFMAs per stage and wave
+    constexpr int kXLoads = TM / 64; // 1 KB direct-to-LDS copies per wave per stage
     constexpr int kQLoads = F::kQLoads, kHLoads = F::kHLoads;
     constexpr int kLook = 6;         // B fragments are read kLook MFMAs before use
     constexpr int kBufBytes = TM * 128;                        // one stage of x
@@ -475,9 +396,10 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     int boff[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) boff[k] = lr * 128 + ((F::chunk(k, h) ^ ((lr >> 1) & 7)) << 4);
-    // MFMA n of a stage (n < 16): k-step n / 4, token fragment n % 4.
+    // MFMA n of a stage (n < MPS): k-step n / NT, token fragment n % NT.
     auto read_b = [&](int buf, int n) {
-        return *reinterpret_cast<const u32x4 *>(lds + buf * kBufBytes + 4096 * (n & 3) + boff[n >> 2]);
+        return *reinterpret_cast<const u32x4 *>(lds + buf * kBufBytes + 4096 * (n % NT) +
+                                                boff[n / NT]);
     };
 
     f32x16 acc[NT];
@@ -521,7 +443,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
             // Copies and weights run 3 stages ahead (ring buffer and q slot
             // (s+3) % 4 held stage s-1, finished during stage s-1), the next
             // super-block's data is issued at il == 0.  Wait for stage s+1's
-            // copies (read from MFMA 16 - kLook of this stage on): the loads
+            // copies (read from MFMA MPS - kLook of this stage on): the loads
             // issued after them are its weights, stage s+2's copies and
             // weights and, at il == 1 and 2, the super-block data.  After the
             // barrier every wave is past stage s-1, whose buffer is refilled.
@@ -535,11 +457,11 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
             q[(il + 3) & 3] = ld.stage(sbi + ((il + 3) >> 2), (il + 3) & 3);
             if (il == 0) hnext = ld.header(sbi + 1);
 
-            // 16 MFMAs of stage s, each followed by a quarter of one 8-weight
-            // A operand of stage s+1 and one B fragment read kLook MFMAs
-            // ahead (into stage s+1 for the last kLook).  The compiler's own
-            // interleave of this stream measured 1-3% faster than one pinned
-            // with sched_barrier.
+            // MPS MFMAs of stage s; one of every MPS / 16 is followed by a
+            // quarter of one 8-weight A operand of stage s+1, and each by one
+            // B fragment read kLook MFMAs ahead (into stage s+1 for the last
+            // kLook).  The compiler's own interleave of this stream measured
+            // 1-3% faster than one pinned with sched_barrier.
             const u32x4 *acur = a[il & 1];
             u32x4 *anext = a[(il + 1) & 1];
             const typename F::Sb &hn = il == 3 ? hnext : hcur;
@@ -548,12 +470,16 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
             const typename F::Scales gs = F::scales(hn, (il + 1) & 3);
             typename F::Piece pc;
 #pragma unroll
-            for (int n = 0; n < 16; ++n) {
-                const int k = n >> 2, tf = n & 3;
-                acc[tf] = mfma32<XT>(acur[k], bq[(16 * il + n) & 7], acc[tf]);
-                F::template piece<XT>(n >> 2, n & 3, (il + 1) & 3, qn, hn, gs, pc, anext[n >> 2]);
+            for (int n = 0; n < MPS; ++n) {
+                const int k = n / NT, tf = n % NT;
+                acc[tf] = mfma32<XT>(acur[k], bq[n & 7], acc[tf]);
+                if (n % (MPS / 16) == 0) {
+                    const int pi = n / (MPS / 16);  // piece pi & 3 of k-step pi >> 2
+                    F::template piece<XT>(pi >> 2, pi & 3, (il + 1) & 3, qn, hn, gs, pc,
+                                          anext[pi >> 2]);
+                }
                 const int nr = n + kLook;
-                bq[(16 * il + nr) & 7] = nr < 16 ? read_b(il, nr) : read_b((il + 1) & 3, nr - 16);
+                bq[nr & 7] = nr < MPS ? read_b(il, nr) : read_b((il + 1) & 3, nr - MPS);
             }
             if (il == 3) hcur = hnext;
         }
@@ -631,9 +557,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
 
 // Split-K reduction for gemm_kernel: block (tile, e), e = tf*4 + j, sums
 // float4 e of every thread of the tile over the splits in split order.
-template <int YT>
+template <int YT, int TM>
 __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
-    constexpr int E = 16;  // float4 per thread
+    constexpr int E = 4 * (TM / 32);  // float4 per thread
     const int tid = threadIdx.x;
     // Block b runs on XCD b % 8 and reduces tiles whose first split ran on
     // that XCD (units [x * units_per_xcd, (x + 1) * units_per_xcd)).
@@ -647,7 +573,7 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
     const int row_tile = tile / p.tok_tiles, tok_tile = tile % p.tok_tiles;
     const int lane = tid & 63, wave = tid >> 6;
     const int row = row_tile * kRowsPerWg + wave * kW8Rows + 8 * j + 4 * (lane >> 5);
-    const int tok = tok_tile * 128 + 32 * tf + (lane & 31);
+    const int tok = tok_tile * TM + 32 * tf + (lane & 31);
     const f32x4 *src = reinterpret_cast<const f32x4 *>(p.ws) +
                        ((int64_t)tile * p.splits * E + e) * 512 + tid;
     f32x4 sum = src[0];
@@ -932,10 +858,9 @@ __global__ __launch_bounds__(256) void tokens_reduce_kernel(void *__restrict__ y
     store_out<YT>(y, i, s);
 }
 
-template <int T, int XT, int YT>
+template <int T, int XT, int YT, int TM>
 static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
                                 int K, hipStream_t st, const Scratch &sc) {
-    constexpr int TM = 128;  // tokens per workgroup tile
     // 32-bit buffer offsets: the x tile, and a wave's 32 rows of Q6_K weights
     const int64_t row_bytes = (int64_t)(K / 256) * GemmFmt<T>::kBytes;
     if ((int64_t)TM * K * 2 > 0x7FFFFFFF || (T == 14 && row_bytes * kW8Rows > 0x7FFFFFFF))
@@ -952,13 +877,13 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     p.tok_tiles = (N + TM - 1) / TM;
     const int tiles = p.row_tiles * p.tok_tiles;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-    // Split K to the nearest whole number of launch waves over the CUs
-    // (cus / tiles rounded), keeping >= 2 super-blocks a split: 128 tiles on
-    // 256 CUs split 2, 172 tiles do not split.
-    int splits = std::max(1, (cus + tiles / 2) / tiles);
+    // Split K into as many parts as keep every unit resident at once (one
+    // workgroup per CU: tiles * splits <= CUs), at least 2 super-blocks a
+    // split: 32 tiles on 256 CUs split 8, 86 split 2, 172 do not split.
+    int splits = std::max(1, cus / tiles);
     splits = std::min(splits, std::max(1, p.nb / 2));
     if (tuning().gemm_splits) splits = tuning().gemm_splits;
-    // the fp32 partials (one 128 KiB tile per unit) must fit the scratch
+    // the fp32 partials (one TM x 256 tile per unit) must fit the scratch
     const size_t unit_bytes = (size_t)TM * kRowsPerWg * sizeof(float);
     splits = (int)std::min<size_t>(splits, std::max<size_t>(1, sc.capacity() / (unit_bytes * tiles)));
     splits = std::max(1, std::min(splits, p.nb));
@@ -971,11 +896,37 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     }
     p.total_units = tiles * splits;
     p.units_per_xcd = (p.total_units + 7) / 8;
-    gemm_kernel<T, XT, YT><<<8 * p.units_per_xcd, 512, 0, st>>>(p);
-    if (splits > 1)  // 16 float4 per thread; at most units_per_xcd / splits + 1 tiles per XCD
-        gemm_reduce_kernel<YT><<<8 * 16 * ((p.units_per_xcd + splits - 1) / splits + 1), 512, 0,
-                                 st>>>(p);
+    gemm_kernel<T, XT, YT, TM><<<8 * p.units_per_xcd, 512, 0, st>>>(p);
+    if (splits > 1) {  // 4 * TM / 32 float4 per thread; at most units_per_xcd / splits + 1 tiles per XCD
+        constexpr int E = 4 * (TM / 32);
+        gemm_reduce_kernel<YT, TM>
+            <<<8 * E * ((p.units_per_xcd + splits - 1) / splits + 1), 512, 0, st>>>(p);
+    }
     return hipGetLastError();
+}
+
+// Token tile.  256 tokens per workgroup halve the dequantisation per MFMA
+// (each wave's 32 dequantised rows feed 8 token fragments): measured, a
+// 256-token tile costs ~1.5x a 128-token one for twice the work.  It is
+// used when the GEMM fills the CUs several times over and needs fewer
+// launch waves that way (m = 4096 on [11008 x 2048]: 3 rounds of 688 tiles
+// instead of 6 of 1376); with fewer tiles than CUs the 128-token tile and
+// its K splits win (the 256-token partials double the split traffic).
+// Q6_K keeps 128 (its format needs more registers).
+template <int T, int XT, int YT>
+static hipError_t launch_gemm_tm(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
+                                 int K, hipStream_t st, const Scratch &sc) {
+    int tm = tuning().gemm_tm;
+    if (tm != 128 && tm != 256) {
+        const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+        const int64_t rows = (M + kRowsPerWg - 1) / kRowsPerWg;
+        const int64_t t128 = rows * ((N + 127) / 128), t256 = rows * ((N + 255) / 256);
+        const int64_t r128 = (t128 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
+        tm = (t128 >= cus && 3 * r256 < 2 * r128) ? 256 : 128;
+    }
+    if constexpr (T != 14)
+        if (tm == 256) return launch_gemm_t<T, XT, YT, 256>(y, w, x, M, N, K, st, sc);
+    return launch_gemm_t<T, XT, YT, 128>(y, w, x, M, N, K, st, sc);
 }
 
 template <int T>
@@ -985,12 +936,12 @@ static hipError_t launch_gemm_xy(void *y, int y_dtype, const uint8_t *w, const v
     const uint16_t *xx = static_cast<const uint16_t *>(x);
     if (x_dtype == RXQ4_DTYPE_BF16) {
         if (y_dtype == RXQ4_DTYPE_BF16)
-            return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, N, K, st, sc);
-        return launch_gemm_t<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st, sc);
+            return launch_gemm_tm<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_BF16>(y, w, xx, M, N, K, st, sc);
+        return launch_gemm_tm<T, RXQ4_DTYPE_BF16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st, sc);
     }
     if (y_dtype == RXQ4_DTYPE_F16)
-        return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, N, K, st, sc);
-    return launch_gemm_t<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st, sc);
+        return launch_gemm_tm<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F16>(y, w, xx, M, N, K, st, sc);
+    return launch_gemm_tm<T, RXQ4_DTYPE_F16, RXQ4_DTYPE_F32>(y, w, xx, M, N, K, st, sc);
 }
 
 hipError_t launch_gemm(int ggml_type, void *y, int y_dtype, const uint8_t *w, const void *x,

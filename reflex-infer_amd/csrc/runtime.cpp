@@ -78,6 +78,7 @@ const Tuning &tuning() {
         r.attn_split = env_pos("RXQ4_ATTN_SPLIT");
         r.attn_mfma = !env_off("RXQ4_ATTN_MFMA");
         r.multi_token_gemv = !env_off("RXQ4_MULTI_TOKEN_GEMV");
+        r.gemm_tm = env_pos("RXQ4_GEMM_TM");
         return r;
     }();
     return t;

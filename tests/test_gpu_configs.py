@@ -431,3 +431,27 @@ def test_reference_dispatcher_computes_on_this_kernel_layer():
         dst=e.data_ptr(), weights=W.data_ptr(), ggml_type=12, token_id=77, hidden_dim=K)) == 0
     torch.cuda.synchronize()
     assert np.array_equal(host16(e), orc.dequant_f16(Wn, K, 77, 1)[0])
+
+
+# ------------------------------------------- the 256-token GEMM tile (large m)
+@pytest.mark.parametrize("t", [12, 13])
+def test_prefill_gemm_256_token_tile(t):
+    """4096 tokens on [4096 x 2048]: 512 tiles of 128 tokens or 256 of 256,
+    so the launcher picks the 256-token tile; sampled rows against the fp64
+    product of the kernel's operands, bf16 and fp32 outputs."""
+    M, N, K = 4096, 4096, 2048
+    W = qweights(9000 + t, M, K, t)
+    g = torch.Generator(device="cuda").manual_seed(9001)
+    x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+    y32 = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    yb = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+    capi.gemm(y32, W, x, M, N, K, ggml_type=t)
+    capi.gemm(yb, W, x, M, N, K, ggml_type=t)
+    rows = np.sort(util.rng(9002).choice(M, 96, replace=False))
+    Wn = sample_rows(W, rows)
+    wb = (orc.kq_dequant_f32(Wn, K, t) if t != 12 else orc.dequant_f32(Wn, K))
+    wb = orc.bits_bf16_to_f32(util.f32_to_bf16_bits(wb)).astype(np.float64).reshape(len(rows), K)
+    ref = x.float().cpu().numpy().astype(np.float64) @ wb.T
+    assert util.rel_err(y32.cpu().numpy()[:, rows], ref) <= util.TOL
+    got = yb.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows]
+    assert util.rounded_ok(got, ref, "bf16").all()
