@@ -117,6 +117,9 @@ LEGS = {
     "embed": (12, VOCAB, HIDDEN, 4096, "embed"),
     "gemm512_11008x2048": (12, FFN, HIDDEN, 512, "gemm"),
     "gemm512_2048x11008": (12, HIDDEN, FFN, 512, "gemm"),
+    "gate_up_m8": (12, 2 * FFN, HIDDEN, 8, "tokens"),
+    "gate_up_m16": (12, 2 * FFN, HIDDEN, 16, "tokens"),
+    "down_m16": (12, HIDDEN, FFN, 16, "tokens"),
 }
 
 
@@ -151,6 +154,10 @@ def run_leg(name: str) -> int:
         xb = gen(1, (m, K), 1.0).to(torch.bfloat16)
         yb = torch.empty((m, M), dtype=torch.bfloat16, device=dev)
         run = lambda i: capi.gemm(yb, ws[i % n_copies], xb, M, m, K)  # noqa: E731
+    elif kind == "tokens":
+        xt = gen(4, (m, K), 1.0).half()
+        yt = torch.empty((m, M), dtype=torch.float16, device=dev)
+        run = lambda i: capi.gemm_f16(yt, ws[i % n_copies], xt, M, m, K)  # noqa: E731
     else:
         x = gen(2, (K,), 1.0).half()
         if kind == "f32":

@@ -576,10 +576,19 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
     const int tok = tok_tile * TM + 32 * tf + (lane & 31);
     const f32x4 *src = reinterpret_cast<const f32x4 *>(p.ws) +
                        ((int64_t)tile * p.splits * E + e) * 512 + tid;
+    // Up to 8 splits' loads are in flight before the first add (a loop of
+    // dependent load-add steps waits out one memory latency per split); the
+    // adds stay in split order.
     f32x4 sum = src[0];
-    for (int sp = 1; sp < p.splits; ++sp) {
-        const f32x4 v = src[(int64_t)sp * E * 512];
-        sum = f32x4{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
+    for (int sp0 = 1; sp0 < p.splits; sp0 += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (sp0 + i < p.splits) v[i] = src[(int64_t)(sp0 + i) * E * 512];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (sp0 + i < p.splits)
+                sum = f32x4{sum[0] + v[i][0], sum[1] + v[i][1], sum[2] + v[i][2], sum[3] + v[i][3]};
     }
     if (tok >= p.N || row >= p.M) return;
     const int valid = min(4, p.M - row);
@@ -853,8 +862,17 @@ __global__ __launch_bounds__(256) void tokens_reduce_kernel(void *__restrict__ y
                                                             int64_t n, int splits) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
+    // up to 8 splits' loads in flight before the adds (in split order)
     float s = ws[i];
-    for (int k = 1; k < splits; ++k) s += ws[(int64_t)k * n + i];
+    for (int k0 = 1; k0 < splits; k0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (k0 + j < splits) v[j] = ws[(int64_t)(k0 + j) * n + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (k0 + j < splits) s += v[j];
+    }
     store_out<YT>(y, i, s);
 }
 

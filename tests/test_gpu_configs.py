@@ -455,3 +455,23 @@ def test_prefill_gemm_256_token_tile(t):
     assert util.rel_err(y32.cpu().numpy()[:, rows], ref) <= util.TOL
     got = yb.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows]
     assert util.rounded_ok(got, ref, "bf16").all()
+
+
+# ------------------------- small batch with x in LDS: super-block counts
+@pytest.mark.parametrize("M,m,K", [(16448, 12, 2816), (16384, 5, 512), (22016, 16, 4096)])
+def test_small_batch_lds_kernel_block_counts(M, m, K):
+    """The LDS small-batch kernel (at least one 64-row workgroup per CU) on
+    rows of 11, 2 and 16 super-blocks (odd counts end on a half-filled
+    prefetch pair), sampled rows against the reference per-token GEMV and
+    the fp64 product of the kernel's operands."""
+    print(f"lds small batch [{M}x{K}] m={m}", flush=True)
+    W = qweights(9200 + m, M, K)
+    x16 = util.x_f16(9201 + m, (m, K))
+    x = dev(x16)
+    y = torch.empty((m, M), dtype=torch.float16, device="cuda")
+    capi.gemm_f16(y, W, x, M, m, K)
+    rows = np.sort(util.rng(9202).choice(M, 256, replace=False))
+    Wn = sample_rows(W, rows)
+    got = host16(y)[:, rows]
+    assert util.rel_err(f16(got), orc.gemm_tokens_f32(Wn, K, x16)) <= util.TOL
+    assert util.rounded_ok(got, orc.gemm_f64(Wn, K, f16(x16), "f16")).all()
