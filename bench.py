@@ -42,6 +42,12 @@ stream and timed with HIP events recorded on that stream around replays:
                same way, with the host CPU model and core count.
 Every extra whose working set could sit in the 256 MB Infinity Cache
 rotates distinct copies totalling more than 512 MB.
+
+Profiling entry points (no timing, for rocprofv3 counter passes):
+  --leg NAME        one kernel's workload, 20 eager launches on distinct weight
+                    copies (gate_up, down, lm_head, embed, the m=512 GEMM
+                    shapes, small batch gate_up_m8 / gate_up_m16 / down_m16)
+  --calibrate-copy  a 256 MiB device copy, to scale FETCH_SIZE / WRITE_SIZE
 """
 from __future__ import annotations
 
