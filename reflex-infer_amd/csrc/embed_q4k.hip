@@ -1,69 +1,98 @@
 // embed_q4k.hip -- Q4_K embedding-row dequantisation for gfx950.
 //
 // Replaces dequant_embedding_q4k_kernel (reference q4_gemm.cu:545-572) and
-// adds the batched gather the reference API cannot express.  A thread owns
-// 16 consecutive outputs of one row: it reads the 16-byte block header and
-// 16 quant bytes, computes w = (d*sc)*q - dmin*m in fp32 (one rounding, as
-// the reference) and writes 16 fp16 (RNE) values with two 16-byte stores.
-// Only the addressed rows are read.  Bytes per launch: unique_rows*K/256*144 (header
-// reads are L2 hits after the first) + n_ids*K*2 written + n_ids*4 ids.
+// adds the batched gather the reference API cannot express.  A thread makes
+// G groups of 8 consecutive outputs of one row: per group one 16-byte block
+// header load, one 8-byte quant load (the group's low or high nibbles),
+// w = (d*sc)*q - dmin*m in fp32 (one rounding, as the reference) and one
+// 16-byte store of 8 fp16 (RNE).  With K a multiple of 512*G the groups of a
+// thread are 512 outputs apart and lane j of a wave writes outputs 8j..8j+7
+// of each 512-output run, so every store instruction writes 1 KB contiguous
+// (16 outputs per thread in one piece, stores 32 bytes apart across the
+// wave, measured 7.06 us against 6.55 us for 4096 fp16 rows of 2048).  All
+// of a thread's loads are issued before its arithmetic.  Only the addressed
+// rows are read.  Bytes per launch: unique_rows*K/256*144 (header reads are
+// L2 hits after the first) + n_ids*K*2 written + n_ids*4 ids.
 #include "launch.h"
 #include "q4k_device.h"
 
 namespace rxq4 {
 
-// A thread owns 16 consecutive outputs (half a sub-block) of one row: the
-// 16-byte header, 16 quant bytes (one load, nibble half of the sub-block)
-// and two 16-byte stores.
-template <bool kBatched>
+// Thread c of row i: output groups e_k = 512*G*(c/64) + 8*(c%64) + 512*k
+// (kContig) or 8*G*c + 8*k, k < G.
+template <bool kBatched, int G, bool kContig>
 __global__ __launch_bounds__(256) void embed_kernel(uint16_t *__restrict__ dst,
                                                     const uint8_t *__restrict__ w,
                                                     const int32_t *__restrict__ ids,
                                                     int token_id, int64_t n_vocab,
                                                     int n_ids, int K) {
-    const int per_row = K >> 4;
+    const int per_row = K / (8 * G);
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t i = t / per_row;
     const int c = (int)(t - i * per_row);
     if (i >= n_ids) return;
-    u32x4 *out = reinterpret_cast<u32x4 *>(dst + i * K + c * 16);
+    // output element groups (8 each) of this thread
+    int e[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k)
+        e[k] = kContig ? (c >> 6) * (512 * G) + 8 * (c & 63) + 512 * k : c * 8 * G + 8 * k;
     int64_t id = token_id;
     if (kBatched) {
         id = ids[i];
         if (id < 0 || id >= n_vocab) {
-            out[0] = u32x4{0, 0, 0, 0};
-            out[1] = u32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int k = 0; k < G; ++k)
+                *reinterpret_cast<u32x4 *>(dst + i * K + e[k]) = u32x4{0, 0, 0, 0};
             return;
         }
     }
     const int nb = K >> 8;
-    const int e0 = c * 16;
-    const int b = e0 >> 8, pos = e0 & 255;
-    const int il = pos >> 6, hi = (pos >> 5) & 1, l0 = pos & 31;
-    const uint8_t *blk = w + (id * nb + b) * kBlockBytes;
-    const u32x4 h = load16(blk);
-    const u32x4 q = load16(blk + 16 + 32 * il + l0);
-    const float d = f16_bits_to_f32(h.x & 0xFFFFu);
-    const float dmin = f16_bits_to_f32(h.x >> 16);
-    uint32_t sc, mn;
-    scale_one(h.y, h.z, h.w, 2 * il + hi, &sc, &mn);
-    const float ds = d * (float)sc;
-    const float dm = dmin * (float)mn;
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    uint32_t packed[8];
+    u32x4 hd[G];
+    u32x2 qv[G];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {  // outputs 2k, 2k + 1 = bytes 2k, 2k + 1
-        const uint32_t word = qw[k >> 1];
-        const int sh = (k & 1) * 16;
-        uint32_t b0 = (word >> sh) & 0xFFu, b1 = (word >> (sh + 8)) & 0xFFu;
-        b0 = hi ? (b0 >> 4) : (b0 & 0xFu);
-        b1 = hi ? (b1 >> 4) : (b1 & 0xFu);
-        const float v0 = ds * (float)b0 - dm;
-        const float v1 = ds * (float)b1 - dm;
-        packed[k] = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
+    for (int k = 0; k < G; ++k) {
+        const int b = e[k] >> 8, pos = e[k] & 255;
+        const uint8_t *blk = w + (id * nb + b) * kBlockBytes;
+        hd[k] = load16(blk);
+        qv[k] = *reinterpret_cast<const u32x2 *>(blk + 16 + 32 * (pos >> 6) + (pos & 31));
     }
-    out[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
-    out[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int pos = e[k] & 255;
+        const int il = pos >> 6, hi = (pos >> 5) & 1;
+        const u32x4 h = hd[k];
+        const float d = f16_bits_to_f32(h.x & 0xFFFFu);
+        const float dmin = f16_bits_to_f32(h.x >> 16);
+        uint32_t sc, mn;
+        scale_one(h.y, h.z, h.w, 2 * il + hi, &sc, &mn);
+        const float ds = d * (float)sc;
+        const float dm = dmin * (float)mn;
+        const uint32_t qw[2] = {qv[k].x, qv[k].y};
+        uint32_t packed[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t word = qw[j >> 1];
+            const int sh = (j & 1) * 16;
+            uint32_t b0 = (word >> sh) & 0xFFu, b1 = (word >> (sh + 8)) & 0xFFu;
+            b0 = hi ? (b0 >> 4) : (b0 & 0xFu);
+            b1 = hi ? (b1 >> 4) : (b1 & 0xFu);
+            const float v0 = ds * (float)b0 - dm;
+            const float v1 = ds * (float)b1 - dm;
+            packed[j] = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
+        }
+        *reinterpret_cast<u32x4 *>(dst + i * K + e[k]) =
+            u32x4{packed[0], packed[1], packed[2], packed[3]};
+    }
+}
+
+template <int G, bool C>
+static void launch_embed_v(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
+                           int64_t n_vocab, int n_ids, int K, hipStream_t st) {
+    const int64_t grid = ((int64_t)n_ids * (K / (8 * G)) + 255) / 256;
+    if (ids)
+        embed_kernel<true, G, C><<<(unsigned)grid, 256, 0, st>>>(dst, w, ids, 0, n_vocab, n_ids, K);
+    else
+        embed_kernel<false, G, C><<<(unsigned)grid, 256, 0, st>>>(dst, w, nullptr, token_id, 0, 1, K);
 }
 
 hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,
@@ -72,10 +101,14 @@ hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int
     const int64_t grid = (threads + 255) / 256;
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
-    if (ids)
-        embed_kernel<true><<<(unsigned)grid, 256, 0, st>>>(dst, w, ids, 0, n_vocab, n_ids, K);
+    // 8-output groups per thread: 4 (stores contiguous across the wave in
+    // 512-output runs) when K allows, else 2, or 2 adjacent ones
+    if (K % 2048 == 0)
+        launch_embed_v<4, true>(dst, w, ids, token_id, n_vocab, n_ids, K, st);
+    else if (K % 1024 == 0)
+        launch_embed_v<2, true>(dst, w, ids, token_id, n_vocab, n_ids, K, st);
     else
-        embed_kernel<false><<<(unsigned)grid, 256, 0, st>>>(dst, w, nullptr, token_id, 0, 1, K);
+        launch_embed_v<2, false>(dst, w, ids, token_id, n_vocab, n_ids, K, st);
     return hipGetLastError();
 }
 

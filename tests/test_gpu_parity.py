@@ -72,7 +72,7 @@ def test_embedding_rows_batched_golden_and_oob(golden):
     assert np.array_equal(host16(out), golden["emb_rows_f16"])
 
 
-@pytest.mark.parametrize("K", [256, 2048, 11008])
+@pytest.mark.parametrize("K", [256, 1024, 2048, 6144, 11008])
 def test_embedding_rows_zipf(K):
     vocab = 3000
     Wn = util.weights(40 + K, vocab, K)
