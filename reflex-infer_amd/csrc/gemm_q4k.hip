@@ -86,6 +86,7 @@ struct GemmParams {
     int M, N, K, nb;
     int row_tiles, tok_tiles, splits, sb_per_split;
     int total_units, units_per_xcd;
+    int tok_major;  // unit order (see gemm_kernel)
 };
 
 constexpr int kW8Rows = 32;                       // weight rows per wave
@@ -333,11 +334,27 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     const int L = blockIdx.x;
     const int V = (L % 8) * p.units_per_xcd + L / 8;  // consecutive units share an XCD
     if (V >= p.total_units) return;
-    // Unit V = tile * splits + split: the splits of a tile run on one XCD,
-    // so their partial tiles stay in that XCD's L2 for the reduction.
-    const int split = V % p.splits;
-    const int tile = V / p.splits;
-    const int row_tile = tile / p.tok_tiles, tok_tile = tile % p.tok_tiles;
+    // Unit order.  Row-major, V = (row_tile * tok_tiles + tok_tile) * splits
+    // + split: an XCD holds all token tiles and splits of its row tiles, so
+    // it reads their weights once and every XCD reads all of x.
+    // Token-major, V = (tok_tile * splits + split) * row_tiles + row_tile:
+    // an XCD holds all row tiles of a few (token tile, split) pairs, so it
+    // reads only their part of x and the weights once per token tile.  The
+    // launcher takes the order with less L2 fill traffic (8 x-reads + the
+    // weights against x + one weight read per token tile).
+    int split, row_tile, tok_tile;
+    if (p.tok_major) {
+        row_tile = V % p.row_tiles;
+        const int r = V / p.row_tiles;
+        split = r % p.splits;
+        tok_tile = r / p.splits;
+    } else {
+        split = V % p.splits;
+        const int t = V / p.splits;
+        row_tile = t / p.tok_tiles;
+        tok_tile = t % p.tok_tiles;
+    }
+    const int tile = row_tile * p.tok_tiles + tok_tile;
     const int sb0 = split * p.sb_per_split;
     const int nsb = min(p.nb, sb0 + p.sb_per_split) - sb0;
     const int n_stages = 4 * nsb;
@@ -562,7 +579,9 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
     constexpr int E = 4 * (TM / 32);  // float4 per thread
     const int tid = threadIdx.x;
     // Block b runs on XCD b % 8 and reduces tiles whose first split ran on
-    // that XCD (units [x * units_per_xcd, (x + 1) * units_per_xcd)).
+    // that XCD in the row-major unit order (units [x * units_per_xcd,
+    // (x + 1) * units_per_xcd)); in the token-major order the same blocks
+    // cover every tile once, without that locality.
     const int xcd = blockIdx.x % 8, jj = blockIdx.x / 8;
     const int t0 = (xcd * p.units_per_xcd + p.splits - 1) / p.splits;
     const int t1 = ((xcd + 1) * p.units_per_xcd + p.splits - 1) / p.splits;
@@ -914,6 +933,9 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     }
     p.total_units = tiles * splits;
     p.units_per_xcd = (p.total_units + 7) / 8;
+    const double x_bytes = 2.0 * N * K, w_bytes = (double)M * row_bytes;
+    p.tok_major = tuning().gemm_order ? tuning().gemm_order == 2
+                                      : x_bytes + p.tok_tiles * w_bytes < 8 * x_bytes + w_bytes;
     gemm_kernel<T, XT, YT, TM><<<8 * p.units_per_xcd, 512, 0, st>>>(p);
     if (splits > 1) {  // 4 * TM / 32 float4 per thread; at most units_per_xcd / splits + 1 tiles per XCD
         constexpr int E = 4 * (TM / 32);

@@ -126,7 +126,8 @@ hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, 
 //   RXQ4_GEMM_SPLITS, RXQ4_GEMV_WAVES_PER_CU, RXQ4_GEMV_LDS_WAVES_PER_CU,
 //   RXQ4_ATTN_SPLIT (cap on decode chunks), RXQ4_ATTN_MFMA=0 (VALU prefill),
 //   RXQ4_MULTI_TOKEN_GEMV=0 (2..4 tokens on the MFMA small-batch kernel),
-//   RXQ4_GEMM_TM=128|256 (the GEMM's token tile).
+//   RXQ4_GEMM_TM=128|256 (the GEMM's token tile),
+//   RXQ4_GEMM_ORDER=1|2 (the GEMM's unit order: row-major | token-major).
 struct Tuning {
     int gemm_splits = 0;
     int gemv_waves_per_cu = 0;
@@ -135,6 +136,7 @@ struct Tuning {
     bool attn_mfma = true;
     bool multi_token_gemv = true;
     int gemm_tm = 0;
+    int gemm_order = 0;
 };
 const Tuning &tuning();
 

@@ -79,6 +79,7 @@ const Tuning &tuning() {
         r.attn_mfma = !env_off("RXQ4_ATTN_MFMA");
         r.multi_token_gemv = !env_off("RXQ4_MULTI_TOKEN_GEMV");
         r.gemm_tm = env_pos("RXQ4_GEMM_TM");
+        r.gemm_order = env_pos("RXQ4_GEMM_ORDER");
         return r;
     }();
     return t;
