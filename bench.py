@@ -46,7 +46,8 @@ rotates distinct copies totalling more than 512 MB.
 Profiling entry points (no timing, for rocprofv3 counter passes):
   --leg NAME        one kernel's workload, 20 eager launches on distinct weight
                     copies (gate_up, down, lm_head, embed, the m=512 GEMM
-                    shapes, small batch gate_up_m8 / gate_up_m16 / down_m16)
+                    shapes, small batch gate_up_m8 / gate_up_m16 / down_m16,
+                    attn_prefill)
   --calibrate-copy  a 256 MiB device copy, to scale FETCH_SIZE / WRITE_SIZE
 """
 from __future__ import annotations
@@ -126,6 +127,7 @@ LEGS = {
     "gate_up_m8": (12, 2 * FFN, HIDDEN, 8, "tokens"),
     "gate_up_m16": (12, 2 * FFN, HIDDEN, 16, "tokens"),
     "down_m16": (12, HIDDEN, FFN, 16, "tokens"),
+    "attn_prefill": (0, 0, 0, 512, "attn_prefill"),
 }
 
 
@@ -139,14 +141,30 @@ def run_leg(name: str) -> int:
     rxq4.load()
     dev = torch.device("cuda:0")
     t, M, K, m, kind = LEGS[name]
-    n_copies = 3 if M == VOCAB else max(2, -(-(600 << 20) // qbytes(M, K)))
 
     def gen(seed, shape, sigma):
         g = torch.Generator(device=dev).manual_seed(seed)
         return torch.randn(shape, generator=g, device=dev) * sigma
 
-    ws = [capi.quantize_ggml(gen(80_000 + i, (M, K), 0.02), t) for i in range(n_copies)]
     launches = 20
+    if kind == "attn_prefill":
+        # causal prefill of m tokens from position 0, 32 query / 8 KV heads,
+        # head_dim 128, fp16 (the bench's attn_prefill_fp16_512 workload)
+        AH, AKV, AD = 32, 8, 128
+        n_copies = 8
+        caches = [(gen(70_000 + i, (m, AKV, AD), 1.0).half(), gen(71_000 + i, (m, AKV, AD), 1.0).half())
+                  for i in range(n_copies)]
+        qp = gen(73_000, (m, AH * AD), 1.0).half()
+        op = torch.empty_like(qp)
+        torch.cuda.synchronize()
+        for i in range(launches):
+            k, v = caches[i % n_copies]
+            capi.attention_prefill_f16(op, qp, k, v, AH, AKV, AD, m, 0, AD ** -0.5)
+        torch.cuda.synchronize()
+        print(json.dumps({"leg": name, "launches": launches, "kv_copies": n_copies}), flush=True)
+        return 0
+    n_copies = 3 if M == VOCAB else max(2, -(-(600 << 20) // qbytes(M, K)))
+    ws = [capi.quantize_ggml(gen(80_000 + i, (M, K), 0.02), t) for i in range(n_copies)]
     if kind == "embed":
         rng = np.random.default_rng(5)
         ranks = np.arange(1, VOCAB + 1, dtype=np.float64)
