@@ -132,7 +132,7 @@ def test_mixed_multi_one_launch(K, Ms, types):
         assert util.rounded_ok(host16(yv), ref).all()
 
 
-@pytest.mark.parametrize("K", [256, 2048, 11008])
+@pytest.mark.parametrize("K", [256, 1024, 2048, 3072, 11008])
 def test_q6k_embedding_bit_exact(K):
     V = 40
     Wn = kb.random_blocks(14, util.rng(730 + K), V, K)
