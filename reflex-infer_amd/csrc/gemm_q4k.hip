@@ -757,20 +757,23 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
 }
 
 // Small batch with x staged in LDS, for matrices with at least one 64-row
-// workgroup per CU (gate+up): the 4 waves split rows (16*RT each, all of K)
+// workgroup per CU (gate+up): the W waves split rows (16*RT each, all of K)
 // and share each super-block's x tile (16 tokens x 512 bytes), copied once
 // per workgroup by direct-to-LDS loads into a ring of 3 buffers, 2
-// super-blocks ahead.  Chunk c (16 bytes) of
-// token t sits at c ^ (t & 15), so a 16-lane fragment read covers the 64
-// banks once.  Weights use the 16-byte (WIDE) layout of gemv_tokens_kernel.
-// Against gemv_tokens_kernel (x fragments from L2 per wave) on 36 distinct
-// gate+up layers: m = 16 17.0 -> 13.3 us, m = 8 13.2 -> 12.8 us; down (32
-// such workgroups, K split needed) stays on gemv_tokens_kernel.
-template <int XT, int YT, int RT>
-__global__ __launch_bounds__(256) void gemv_tokens_lds_kernel(
+// super-blocks ahead.  Chunk c (16 bytes) of token t sits at c ^ (t & 15),
+// so a 16-lane fragment read covers the 64 banks once.  Weights use the
+// 16-byte (WIDE) layout of gemv_tokens_kernel.  Against gemv_tokens_kernel
+// (x fragments from L2 per wave) on 36 distinct gate+up layers: m = 16
+// 17.0 -> 13.3 us, m = 8 13.2 -> 12.8 us; down (32 such workgroups, K split
+// needed) stays on gemv_tokens_kernel.
+template <int XT, int YT, int RT, int W>
+__global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
     void *__restrict__ y, const uint8_t *__restrict__ w, const uint16_t *__restrict__ x, int M,
     int N, int K) {
-    constexpr int kBuf = 3;
+    constexpr int D = 2;             // super-blocks in flight per wave
+    constexpr int kBuf = D + 1;
+    constexpr int kXc = 8 / W;       // x copy instructions per wave and super-block
+    static_assert(kXc * W == 8, "workgroup shape");
     __shared__ __attribute__((aligned(1024))) uint8_t xs[kBuf][16 * 512];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -778,38 +781,44 @@ __global__ __launch_bounds__(256) void gemv_tokens_lds_kernel(
     const int li = lane & 15;
     const int g = lane >> 4;
     const int nb = K >> 8;
-    const int row0 = blockIdx.x * 64 * RT + wave * 16 * RT;
+    const int row0 = (blockIdx.x * W + wave) * 16 * RT;
     const int64_t row_bytes = (int64_t)nb * kBlockBytes;
     const uint8_t *wr[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) wr[t] = w + min(row0 + 16 * t + li, M - 1) * row_bytes;
-    const int n_sb = nb;
 
-    // x copies: instruction u of wave w covers tokens 2j, 2j + 1 (j = w + 4u);
+    // x copies: instruction u of wave w covers tokens 2j, 2j + 1 (j = w + W*u);
     // lane i: token 2j + i/32 (clamped to N - 1), LDS chunk i % 32.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, N * K * 2);
-    int xoff[2];
+    int xoff[kXc];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int t = 2 * (wave + 4 * u) + (lane >> 5), p = lane & 31;
+    for (int u = 0; u < kXc; ++u) {
+        const int t = 2 * (wave + W * u) + (lane >> 5), p = lane & 31;
         xoff[u] = (min(t, N - 1) * K + 8 * (p ^ (t & 15))) * 2;
     }
+    // Super-blocks past the end are still loaded, from one fixed line (the
+    // first 512 B of x, the first block of w), so that every step issues the
+    // same number of loads and all vmcnt waits stay exact (a branch around
+    // the loads made the compiler's waits drain the prefetch: 9.7 -> 8.0 us
+    // at m = 5 on [16384 x 2048]); their copies land in a ring buffer no
+    // step reads again.
     auto issue_x = [&](int i) {
-        const int sb = min(i, nb - 1);
+        const bool live = i < nb;  // uniform
         uint8_t *dst = xs[i % kBuf];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-            buffer_to_lds16(xr, dst + (wave + 4 * u) * 1024, xoff[u], sb * 512);
+        for (int u = 0; u < kXc; ++u)
+            buffer_to_lds16(xr, dst + (wave + W * u) * 1024, live ? xoff[u] : 16 * (lane & 31),
+                            live ? i * 512 : 0);
     };
     struct Sb {
         u32x4 hdr[RT];
         u32x4 qw[RT][2];
     };
     auto load = [&](int i, Sb &o) {
-        const int sb = min(i, nb - 1);
+        const bool live = i < nb;  // uniform
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const uint8_t *blk = wr[t] + sb * kBlockBytes;
+            const uint8_t *blk = live ? wr[t] + i * kBlockBytes : w;
             o.hdr[t] = load16(blk);
             o.qw[t][0] = load16(blk + 16 + 32 * g);
             o.qw[t][1] = load16(blk + 32 + 32 * g);
@@ -840,25 +849,27 @@ __global__ __launch_bounds__(256) void gemv_tokens_lds_kernel(
         }
     };
     // Per step i: this wave's copies of super-block i have landed once the
-    // loads issued after them (its weights, the next copies and weights:
-    // 3*RT + 2 + 3*RT) are at most outstanding; the barrier makes all four
-    // waves' copies visible and says every wave is done with buffer
-    // (i - 1) % 3, which the copies of i + 2 refill.
+    // loads issued after them (its weights, then copies and weights of the
+    // D - 1 super-blocks after it: 3*RT + (D-1)*(3*RT + kXc)) are at most
+    // outstanding; the barrier makes all W waves' copies visible and says
+    // every wave is done with buffer (i - 1) % (D + 1), which the copies of
+    // i + D refill.  Steps past nb (the last round) only load.
     auto step = [&](int i, Sb &S) {
-        wait_vmcnt<6 * RT + 2>();
+        wait_vmcnt<3 * RT + (D - 1) * (3 * RT + kXc)>();
         lds_barrier();
-        issue_x(i + 2);
-        compute(S, i);
-        load(i + 2, S);
+        issue_x(i + D);
+        if (i < nb) compute(S, i);  // uniform
+        load(i + D, S);
     };
-    Sb A, B;
-    issue_x(0);
-    load(0, A);
-    issue_x(1);
-    load(1, B);
-    for (int i = 0; i < n_sb; i += 2) {
-        step(i, A);
-        if (i + 1 < n_sb) step(i + 1, B);  // uniform in the workgroup
+    Sb S[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        issue_x(j);
+        load(j, S[j]);
+    }
+    for (int i0 = 0; i0 < nb; i0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) step(i0 + j, S[j]);
     }
     wait_vmcnt<0>();  // trailing copies must land before the workgroup exits
 
@@ -1012,7 +1023,16 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
     const bool wide = n_tok <= 8;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
     if ((M + 63) / 64 >= cus) {
-        gemv_tokens_lds_kernel<XT, YT, 1><<<(M + 63) / 64, 256, 0, st>>>(y, w, x, M, n_tok, K);
+        // 64-row workgroups of 4 waves; between one and two of them per CU,
+        // 128-row workgroups of 8 waves (at most one per CU) instead: [22016 x
+        // 2048] m = 16 13.5 -> 11.8 us (344 workgroups put two on 88 CUs).
+        const int g64 = (M + 63) / 64;
+        const bool eight = tuning().tokens_waves ? tuning().tokens_waves == 8
+                                                 : g64 > cus && g64 <= 2 * cus;
+        if (eight)
+            gemv_tokens_lds_kernel<XT, YT, 1, 8><<<(M + 127) / 128, 512, 0, st>>>(y, w, x, M, n_tok, K);
+        else
+            gemv_tokens_lds_kernel<XT, YT, 1, 4><<<g64, 256, 0, st>>>(y, w, x, M, n_tok, K);
         return hipGetLastError();
     }
     int splits = 1;

@@ -137,6 +137,7 @@ struct Tuning {
     bool multi_token_gemv = true;
     int gemm_tm = 0;
     int gemm_order = 0;
+    int tokens_waves = 0;
 };
 const Tuning &tuning();
 

@@ -80,6 +80,7 @@ const Tuning &tuning() {
         r.multi_token_gemv = !env_off("RXQ4_MULTI_TOKEN_GEMV");
         r.gemm_tm = env_pos("RXQ4_GEMM_TM");
         r.gemm_order = env_pos("RXQ4_GEMM_ORDER");
+        r.tokens_waves = env_pos("RXQ4_TOKENS_WAVES");
         return r;
     }();
     return t;
