@@ -8,6 +8,11 @@
 //       t + threads, ..., coalesced per load; u <= 16) before any use; one
 //       dword per workgroup goes to `sink` so the loads stay live.  bench.py
 //       takes the fastest of a few grid sizes.
+//   rxq4_floor_read_runs(src, bytes, sink, run_kb, stream)    reads `bytes`
+//       (a multiple of 1024) as contiguous runs of `run_kb` KB (1..32), one
+//       run per wave, 4 waves per workgroup: lane l of the wave loads 16
+//       bytes at run + 1024*j + 16*l for every j, all before any use (the
+//       access pattern of a GEMV wave that streams whole rows).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -39,6 +44,30 @@ __global__ __launch_bounds__(256) void floor_read_kernel(const u32x4 *__restrict
     }
 }
 
+template <int R>
+__global__ __launch_bounds__(256) void floor_runs_kernel(const uint8_t *__restrict__ src,
+                                                         int64_t n_runs, uint32_t *sink) {
+    const int lane = threadIdx.x & 63;
+    const int64_t run = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    uint32_t acc = 0;
+    if (run < n_runs) {
+        const uint8_t *p = src + run * (R * 1024) + 16 * lane;
+        u32x4 v[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) v[j] = *reinterpret_cast<const u32x4 *>(p + 1024 * j);
+#pragma unroll
+        for (int j = 0; j < R; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    __shared__ uint32_t red[256];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t s = 0;
+        for (int i = 0; i < 256; ++i) s ^= red[i];
+        sink[blockIdx.x] = s;
+    }
+}
+
 extern "C" {
 
 int rxq4_floor_empty(void *stream) {
@@ -60,6 +89,27 @@ int rxq4_floor_read(const void *src, int64_t bytes, uint32_t *sink, int blocks, 
     else if (u <= 8) floor_read_kernel<8><<<blocks, 256, 0, st>>>(s, n16, sink);
     else if (u <= 16) floor_read_kernel<16><<<blocks, 256, 0, st>>>(s, n16, sink);
     else return 4;
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// sink: at least ceil(bytes / (run_kb KB) / 4) dwords
+int rxq4_floor_read_runs(const void *src, int64_t bytes, uint32_t *sink, int run_kb, void *stream) {
+    if (bytes <= 0 || (reinterpret_cast<uintptr_t>(src) & 15) != 0) return 4;
+    if (run_kb < 1 || run_kb > 32 || bytes % ((int64_t)run_kb * 1024) != 0) return 4;
+    const int64_t n_runs = bytes / ((int64_t)run_kb * 1024);
+    const int64_t blocks = (n_runs + 3) / 4;
+    if (blocks > 0x7FFFFFFF) return 4;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint8_t *s = static_cast<const uint8_t *>(src);
+    switch (run_kb) {
+    case 1: floor_runs_kernel<1><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
+    case 2: floor_runs_kernel<2><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
+    case 4: floor_runs_kernel<4><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
+    case 8: floor_runs_kernel<8><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
+    case 16: floor_runs_kernel<16><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
+    case 32: floor_runs_kernel<32><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
+    default: return 4;
+    }
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
