@@ -769,7 +769,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_tokens_kernel(
 template <int XT, int YT, int RT, int W>
 __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
     void *__restrict__ y, const uint8_t *__restrict__ w, const uint16_t *__restrict__ x, int M,
-    int N, int K) {
+    int N, int K, float *__restrict__ ws, int sb_per_split) {
     constexpr int D = 2;             // super-blocks in flight per wave
     constexpr int kBuf = D + 1;
     constexpr int kXc = 8 / W;       // x copy instructions per wave and super-block
@@ -781,6 +781,10 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
     const int li = lane & 15;
     const int g = lane >> 4;
     const int nb = K >> 8;
+    // super-blocks [sb_lo, sb_lo + n_sb) of K split blockIdx.y (all of K
+    // without a split)
+    const int sb_lo = blockIdx.y * sb_per_split;
+    const int n_sb = min(nb, sb_lo + sb_per_split) - sb_lo;
     const int row0 = (blockIdx.x * W + wave) * 16 * RT;
     const int64_t row_bytes = (int64_t)nb * kBlockBytes;
     const uint8_t *wr[RT];
@@ -803,22 +807,22 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
     // at m = 5 on [16384 x 2048]); their copies land in a ring buffer no
     // step reads again.
     auto issue_x = [&](int i) {
-        const bool live = i < nb;  // uniform
+        const bool live = i < n_sb;  // uniform
         uint8_t *dst = xs[i % kBuf];
 #pragma unroll
         for (int u = 0; u < kXc; ++u)
             buffer_to_lds16(xr, dst + (wave + W * u) * 1024, live ? xoff[u] : 16 * (lane & 31),
-                            live ? i * 512 : 0);
+                            live ? (sb_lo + i) * 512 : 0);
     };
     struct Sb {
         u32x4 hdr[RT];
         u32x4 qw[RT][2];
     };
     auto load = [&](int i, Sb &o) {
-        const bool live = i < nb;  // uniform
+        const bool live = i < n_sb;  // uniform
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const uint8_t *blk = live ? wr[t] + i * kBlockBytes : w;
+            const uint8_t *blk = live ? wr[t] + (sb_lo + i) * kBlockBytes : w;
             o.hdr[t] = load16(blk);
             o.qw[t][0] = load16(blk + 16 + 32 * g);
             o.qw[t][1] = load16(blk + 32 + 32 * g);
@@ -853,12 +857,12 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
     // D - 1 super-blocks after it: 3*RT + (D-1)*(3*RT + kXc)) are at most
     // outstanding; the barrier makes all W waves' copies visible and says
     // every wave is done with buffer (i - 1) % (D + 1), which the copies of
-    // i + D refill.  Steps past nb (the last round) only load.
+    // i + D refill.  Steps past n_sb (the last round) only load.
     auto step = [&](int i, Sb &S) {
         wait_vmcnt<3 * RT + (D - 1) * (3 * RT + kXc)>();
         lds_barrier();
         issue_x(i + D);
-        if (i < nb) compute(S, i);  // uniform
+        if (i < n_sb) compute(S, i);  // uniform
         load(i + D, S);
     };
     Sb S[D];
@@ -867,7 +871,7 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
         issue_x(j);
         load(j, S[j]);
     }
-    for (int i0 = 0; i0 < nb; i0 += D) {
+    for (int i0 = 0; i0 < n_sb; i0 += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) step(i0 + j, S[j]);
     }
@@ -879,7 +883,11 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = row0 + 16 * t + 4 * g + r;
-            if (row < M) store_out<YT>(y, (int64_t)li * M + row, acc[t][r]);
+            if (row >= M) continue;
+            if (ws)  // split K: fp32 partial [split][token][row]
+                ws[((int64_t)blockIdx.y * N + li) * M + row] = acc[t][r];
+            else
+                store_out<YT>(y, (int64_t)li * M + row, acc[t][r]);
         }
     }
 }
@@ -1030,9 +1038,33 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
         const bool eight = tuning().tokens_waves ? tuning().tokens_waves == 8
                                                  : g64 > cus && g64 <= 2 * cus;
         if (eight)
-            gemv_tokens_lds_kernel<XT, YT, 1, 8><<<(M + 127) / 128, 512, 0, st>>>(y, w, x, M, n_tok, K);
+            gemv_tokens_lds_kernel<XT, YT, 1, 8>
+                <<<(M + 127) / 128, 512, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
         else
-            gemv_tokens_lds_kernel<XT, YT, 1, 4><<<g64, 256, 0, st>>>(y, w, x, M, n_tok, K);
+            gemv_tokens_lds_kernel<XT, YT, 1, 4><<<g64, 256, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
+        return hipGetLastError();
+    }
+    if (nb >= 16) {
+        // Long rows: 64-row workgroups with x staged in LDS and K split over
+        // workgroups (about one per CU, at least 4 super-blocks a split).
+        const int g64 = (M + 63) / 64;
+        int splits = tuning().tokens_lds_split ? std::min(tuning().tokens_lds_split, nb)
+                                               : std::max(1, std::min(cus / g64, nb / 4));
+        splits = (int)std::min<size_t>(
+            splits, std::max<size_t>(1, sc.capacity() / ((size_t)n_tok * M * sizeof(float))));
+        const int sbps = (nb + splits - 1) / splits;
+        splits = (nb + sbps - 1) / sbps;
+        float *ws = nullptr;
+        if (splits > 1) {
+            hipError_t e = sc.get(st, (size_t)splits * n_tok * M * sizeof(float), &ws);
+            if (e != hipSuccess) return e;
+        }
+        gemv_tokens_lds_kernel<XT, YT, 1, 4>
+            <<<dim3(g64, splits), 256, 0, st>>>(y, w, x, M, n_tok, K, ws, sbps);
+        if (splits > 1) {
+            const int64_t n = (int64_t)n_tok * M;
+            tokens_reduce_kernel<YT><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(y, ws, n, splits);
+        }
         return hipGetLastError();
     }
     int splits = 1;

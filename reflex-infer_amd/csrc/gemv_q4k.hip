@@ -678,6 +678,17 @@ static hipError_t launch_multi_epi(GemvParams &p, int n_tok, hipStream_t st) {
     }
 }
 
+// 2 tokens: the multi-token GEMV.  3: it too when the rows give at least
+// one 64-row workgroup per CU (gate+up [22016 x 2048]: 10.2 against 11.4 us
+// on the MFMA small-batch kernel), else the MFMA kernel (down [2048 x
+// 11008] 9.0 against 9.3 us, QKV 4.4 against 5.0 us).  4: the MFMA kernel
+// (gate+up 11.3 against 11.6 us, down 9.1 against 11.1 us).  Graph replay,
+// distinct weights.
+bool gemv_multi_token_preferred(int n_tok, int M) {
+    const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+    return n_tok == 2 || (n_tok == 3 && (M + 63) / 64 >= cus);
+}
+
 bool gemv_multi_token_fits(int n_tok, int K) {
     const int slots = 4 * (K / 256);
     if (slots <= 64 && (64 % slots) == 0) return true;

@@ -72,6 +72,9 @@ hipError_t launch_gemv_multi_token(void *y, int y_dtype, const uint8_t *w, const
 // K/256 <= 16 blocks keep x in registers; longer rows stage every token's x
 // in LDS (n_tok * K/256 * 576 bytes, at most 160 KiB).
 bool gemv_multi_token_fits(int n_tok, int K);
+// Whether n_tok tokens on M rows run faster on the multi-token GEMV than on
+// the MFMA small-batch kernel (measured crossover).
+bool gemv_multi_token_preferred(int n_tok, int M);
 
 struct DeviceInfo {
     int cu_count;
@@ -134,10 +137,11 @@ struct Tuning {
     int gemv_lds_waves_per_cu = 0;
     int attn_split = 0;
     bool attn_mfma = true;
-    bool multi_token_gemv = true;
+    int multi_token_gemv = -1;  // 2..4 tokens on the multi-token GEMV: -1 measured crossover, 0 never, 1 always
     int gemm_tm = 0;
     int gemm_order = 0;
     int tokens_waves = 0;
+    int tokens_lds_split = 0;
 };
 const Tuning &tuning();
 

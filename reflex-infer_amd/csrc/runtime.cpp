@@ -77,10 +77,12 @@ const Tuning &tuning() {
         r.gemv_lds_waves_per_cu = env_pos("RXQ4_GEMV_LDS_WAVES_PER_CU");
         r.attn_split = env_pos("RXQ4_ATTN_SPLIT");
         r.attn_mfma = !env_off("RXQ4_ATTN_MFMA");
-        r.multi_token_gemv = !env_off("RXQ4_MULTI_TOKEN_GEMV");
+        r.multi_token_gemv = env_off("RXQ4_MULTI_TOKEN_GEMV") ? 0
+                             : env_pos("RXQ4_MULTI_TOKEN_GEMV") ? 1 : -1;
         r.gemm_tm = env_pos("RXQ4_GEMM_TM");
         r.gemm_order = env_pos("RXQ4_GEMM_ORDER");
         r.tokens_waves = env_pos("RXQ4_TOKENS_WAVES");
+        r.tokens_lds_split = env_pos("RXQ4_TOKENS_LDS_SPLIT");
         return r;
     }();
     return t;

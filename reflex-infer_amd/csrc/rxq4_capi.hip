@@ -212,9 +212,11 @@ int gemm_impl(const char *fn, void *y, int y_dtype, const void *w, int ggml_type
         e = rxq4::launch_gemm(ggml_type, y, y_dtype, static_cast<const uint8_t *>(w), x, x_dtype,
                               M, N, K, st, sc);
     else if (N <= rxq4::kMaxRegTokens && x_dtype == RXQ4_DTYPE_F16 &&
-             rxq4::tuning().multi_token_gemv && rxq4::gemv_multi_token_fits(N, K))
-        // 2..4 fp16 tokens: the decode GEMV with every token's activations in
-        // registers (one weight read, the nibble decode shared by the tokens)
+             (rxq4::tuning().multi_token_gemv > 0 ||
+              (rxq4::tuning().multi_token_gemv < 0 && rxq4::gemv_multi_token_preferred(N, M))) &&
+             rxq4::gemv_multi_token_fits(N, K))
+        // 2 (or 3) fp16 tokens: the decode GEMV with every token's activations
+        // in registers (one weight read, the nibble decode shared by the tokens)
         e = rxq4::launch_gemv_multi_token(y, y_dtype, static_cast<const uint8_t *>(w),
                                           static_cast<const uint16_t *>(x), M, N, K, st);
     else if (N <= rxq4::kMaxSmallBatch)

@@ -88,10 +88,10 @@ def test_config2_small_batch_decode(name, M, K, m):
     got = host16(y)[:, rows]
     ref32 = orc.gemm_tokens_f32(Wn, K, x16)       # the reference's per-token CPU GEMV
     assert util.rel_err(f16(got), ref32) <= util.TOL
-    # the kernel's operands: up to 4 tokens the decode GEMV on exact weights
-    # (rows of 8 blocks) or its LDS variant (43 blocks), above that the MFMA
+    # the kernel's operands: the multi-token decode GEMV on exact weights
+    # (rows of 8 blocks) or its LDS variant (43 blocks), else the MFMA
     # kernel on fp16-rounded weights
-    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if m <= 4
+    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if util.gemv_path(m, M, K)
              else orc.gemm_f64(Wn, K, f16(x16), "f16"))
     assert util.rounded_ok(got, ref64).all()
 
@@ -366,10 +366,30 @@ def test_small_batch_long_rows(M, N, K):
     ref32 = orc.gemm_tokens_f32(Wn, K, x16)
     assert util.rel_err(f16(host16(y)), ref32) <= util.TOL
     # the multi-token GEMV stages N rows of x in LDS (N * K/256 * 576 bytes);
-    # past 160 KiB the MFMA small-batch kernel (fp16 weight tiles) takes over
-    fits = N * (K // 256) * 576 <= 160 * 1024
-    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if fits
+    # past 160 KiB, or past its token crossover, the MFMA small-batch kernel
+    # (fp16 weight tiles) takes over
+    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if util.gemv_path(N, M, K)
              else orc.gemm_f64(Wn, K, f16(x16), "f16"))
+    assert util.rounded_ok(host16(y), ref64).all()
+
+
+# ------------------------------- long rows, m >= 5: LDS x tile, K split
+# Rows of >= 16 super-blocks and fewer than one 64-row workgroup per CU run
+# the LDS-staged kernel with K split over workgroups (fp32 partials added in
+# split order): ragged row counts, odd super-block counts, a last split of
+# one super-block, and 64 splits.
+@pytest.mark.parametrize("M,N,K", [(200, 7, 4352), (100, 12, 16384), (64, 5, 65536),
+                                   (2048, 16, 11008), (1000, 9, 5888)])
+def test_small_batch_long_rows_lds_split(M, N, K):
+    print(f"small batch lds split M={M} N={N} K={K}", flush=True)
+    Wn = util.weights(7100 + N + K // 256, M, K)
+    x16 = util.x_f16(7101 + N, (N, K))
+    W, x = dev(Wn), dev(x16)
+    y = torch.empty((N, M), dtype=torch.float16, device="cuda")
+    assert capi.gemm_f16(y, W, x, M, N, K) == 0
+    ref32 = orc.gemm_tokens_f32(Wn, K, x16)
+    assert util.rel_err(f16(host16(y)), ref32) <= util.TOL
+    ref64 = orc.gemm_f64(Wn, K, f16(x16), "f16")
     assert util.rounded_ok(host16(y), ref64).all()
 
 

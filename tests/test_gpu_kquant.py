@@ -240,8 +240,8 @@ def test_gemm_random_shapes_all_paths():
             x = dev(x16).view(torch.float16)
             xv = f16(x16)
         capi.gemm(y, W, x, M, N, K, ggml_type=t)
-        # Q4_K with up to 4 fp16 tokens runs the GEMV (weights unrounded),
+        # Q4_K with 1-3 fp16 tokens may run the GEMV (weights unrounded),
         # everything else the MFMA kernels on weights rounded to the x type
-        wkind = None if (t == 12 and xt == "f16" and N <= 4) else xt
+        wkind = None if (t == 12 and xt == "f16" and util.gemv_path(N, M, K)) else xt
         ref = orc.kq_gemm_f64(Wn, K, t, xv, wkind)
         assert util.rel_err(y.cpu().numpy(), ref) <= util.TOL, f"case {case}"

@@ -10,6 +10,8 @@ from __future__ import annotations
 
 import ctypes
 import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -20,6 +22,8 @@ from oracle import oracle as orc
 from rxq4 import api, capi
 from tests import kquant_blocks as kb
 from tests import util
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 pytestmark = pytest.mark.gpu
 
@@ -314,9 +318,9 @@ def test_api_gemm_quant_batched_f16(M, N, K):
     Wn = util.weights(110 + N, M, K)
     x16 = util.x_f16(111 + N, (N, K))
     ref32 = orc.gemm_tokens_f32(Wn, K, x16)   # reference CPU semantics (per-token GEMV)
-    # the same operands as the kernel: up to 4 tokens run the decode GEMV on
-    # the exact weights, more tokens the MFMA tiles on fp16-rounded weights
-    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if N <= 4
+    # the same operands as the kernel: the decode GEMV on the exact weights
+    # (util.gemv_path), else the MFMA tiles on fp16-rounded weights
+    ref64 = (orc.kq_gemm_f64(Wn, K, 12, f16(x16), None) if util.gemv_path(N, M, K)
              else orc.gemm_f64(Wn, K, f16(x16), "f16"))
     W, x = dev(Wn), dev(x16)
     y = torch.empty((N, M), dtype=torch.float16, device="cuda")
@@ -328,11 +332,31 @@ def test_api_gemm_quant_batched_f16(M, N, K):
     assert util.rounded_ok(host16(y), ref64).all()
 
 
-# 2..4 fp16 tokens: the decode GEMV kernels with every token's activations in
-# registers (register kernel for K 256..4096, LDS kernel for 1536 / 11008).
-@pytest.mark.parametrize("M,N,K", [(300, 2, 2048), (2048, 4, 2048), (129, 3, 11008),
-                                   (70, 4, 1536), (33, 2, 256), (17, 4, 4096), (5000, 2, 512)])
+# 2..4 fp16 tokens on the multi-token decode GEMV (every token's activations
+# in registers: register kernel for K 256..4096, LDS kernel for 1536 / 11008).
+# The launcher picks it for 2 tokens (3 on wide matrices); the cases it sends
+# to the MFMA kernel run in a child process with RXQ4_MULTI_TOKEN_GEMV=1.
+MT_CASES = [(300, 2, 2048), (2048, 4, 2048), (129, 3, 11008), (70, 4, 1536), (33, 2, 256),
+            (17, 4, 4096), (5000, 2, 512)]
+
+
+@pytest.mark.parametrize("M,N,K", MT_CASES)
 def test_multi_token_gemv_equals_per_token_gemv(M, N, K):
+    if not util.gemv_path(N, M, K):
+        env = dict(os.environ, RXQ4_MULTI_TOKEN_GEMV="1")
+        code = ("import sys; sys.path[:0] = [%r, %r]\n"
+                "from tests import test_gpu_parity as t\n"
+                "t.check_multi_token_gemv(%d, %d, %d)\nprint('multi-token ok')\n"
+                % (ROOT, os.path.join(ROOT, "reflex-infer_amd"), M, N, K))
+        r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True,
+                           text=True, timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        assert "multi-token ok" in r.stdout
+        return
+    check_multi_token_gemv(M, N, K)
+
+
+def check_multi_token_gemv(M, N, K):
     print(f"multi-token GEMV M={M} N={N} K={K}", flush=True)
     Wn = util.weights(140 + N + K, M, K)
     x16 = util.x_f16(141 + N, (N, K))

@@ -90,3 +90,19 @@ def zipf_ids(seed: int, n: int, vocab: int, s: float = 1.1) -> np.ndarray:
     rank_idx = np.minimum(np.searchsorted(cdf, u, side="left"), vocab - 1)
     perm = r.permutation(vocab)
     return perm[rank_idx].astype(np.int32)
+
+
+def gemv_path(N: int, M: int, K: int) -> bool:
+    """Whether rxq4_gemm_f16 runs Q4_K with N fp16 tokens on the decode GEMV
+    kernels (exact weights) rather than the MFMA kernels (fp16-rounded
+    weights): one token always; 2 tokens, and 3 when the rows give at least
+    one 64-row workgroup per CU, on the multi-token GEMV while its x fits
+    (registers up to 16 blocks a row, else N * K/256 * 576 bytes of LDS)."""
+    if N == 1:
+        return True
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if not (N == 2 or (N == 3 and -(-M // 64) >= cus)):
+        return False
+    slots = 4 * (K // 256)
+    return (slots <= 64 and 64 % slots == 0) or N * (K // 256) * 576 <= 160 * 1024
