@@ -664,6 +664,28 @@ def main() -> int:
                 tf = 2 * 512 * M * K / med / 1e6
                 kernels[f"{tname}_gemm_bf16_m512_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1)}
                 del ws
+        # Reference point outside the path: the vendor library's dense bf16
+        # GEMM (2-D torch.mm, hipBLASLt) on the same shapes,
+        # weights already bf16 (no dequantisation) and laid out like the
+        # Q4_K rows ([M x K], the library's faster layout of the two: [K x M]
+        # measured 43 / 76 us at m = 512); copies rotate over > 512 MB.
+        vendor = {}
+        for (M, K) in ((FFN, HIDDEN), (HIDDEN, FFN)):
+            n_w = max(2, -(-600_000_000 // (M * K * 2)))
+            wts = [gen(32_000 + M + i, (M, K), 0.02).to(torch.bfloat16) for i in range(n_w)]
+            for m in (512, 2048):
+                xb = gen(42_000 + K + m, (m, K), 1.0).to(torch.bfloat16)
+                yb = torch.empty((m, M), dtype=torch.bfloat16, device=dev)
+
+                def vd_launch(i, xb=xb, yb=yb):
+                    torch.mm(xb, wts[i % n_w].t(), out=yb)
+                med, _ = per_launch(vd_launch, 2 * n_w)
+                tf = 2 * m * M * K / med / 1e6
+                vendor[f"m{m}_{M}x{K}"] = {"us": round(med, 3), "TFLOPs": round(tf, 1),
+                                           "q4k_gemm_us": kernels[f"gemm_bf16_m{m}_{M}x{K}"]["us"]}
+                del xb, yb
+            del wts
+        extras["vendor_bf16_gemm"] = vendor
 
     # ------------------------------------------------------- CPU baseline
     cpu = None
