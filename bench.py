@@ -603,6 +603,26 @@ def main() -> int:
         fl = 4.0 * AH * AD * sum(t + 1 for t in range(512))
         kernels["attn_prefill_fp16_512"] = {"us": round(med, 3), "TFLOPs": round(fl / med / 1e6, 2)}
         del caches
+        # Reference point outside the path: the framework's fused causal
+        # attention on the same problem (torch SDPA restricted to its flash
+        # backend, which raises rather than fall back; K/V expanded to the
+        # 32 query heads, its GQA form), timed the same way.
+        try:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            vq = [gen(76_000 + i, (1, AH, 512, AD), 1.0).half() for i in range(8)]
+            vkv = [tuple(gen(s0 + i, (1, AKV, 512, AD), 1.0).half()
+                         .repeat_interleave(AH // AKV, dim=1).contiguous() for s0 in (77_000, 78_000))
+                   for i in range(8)]
+
+            def sdpa_launch(i):
+                k, v = vkv[i % 8]
+                torch.nn.functional.scaled_dot_product_attention(vq[i % 8], k, v, is_causal=True)
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                med, _ = per_launch(sdpa_launch, 8)
+            extras["vendor_sdpa_prefill_512"] = {"us": round(med, 3), "TFLOPs": round(fl / med / 1e6, 2)}
+            del vq, vkv
+        except Exception as ex:  # no flash backend on this build: report, do not fall back
+            extras["vendor_sdpa_prefill_512"] = {"unavailable": f"{type(ex).__name__}: {str(ex)[:120]}"}
         # 9 K/V pairs of 67 MB (604 MB)
         long_kv = [(gen(74_000 + i, (16384, AKV, AD), 1.0).half(), gen(75_000 + i, (16384, AKV, AD), 1.0).half())
                    for i in range(9)]
