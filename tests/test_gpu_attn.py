@@ -129,10 +129,14 @@ def test_decode_api_matches_c_abi():
 # (n_heads, n_kv, head_dim, N, start_pos, int8): GQA groups 1, 2 (6 heads per
 # KV head: two head blocks), 4, 8 and 32 (two blocks of 16), head_dim 64 and
 # 128 (matrix-core prefill) and 80 (VALU kernel), N not a multiple of the
-# token block, int8 with and without scales.
+# token block, int8 with and without scales.  The last two have more
+# workgroups (8 KV heads x 33-34 blocks of 16 tokens) than the 256 CUs and
+# take the one-group kernel (V^T staged by the threads); the others the
+# two-group kernel (V read back with transposing LDS reads).
 PREFILL = [(32, 8, 128, 100, 0, False), (16, 4, 128, 300, 37, False), (8, 8, 64, 70, 5, False),
            (16, 2, 64, 33, 200, False), (32, 1, 128, 20, 10, False), (12, 2, 128, 17, 3, False),
-           (16, 4, 128, 50, 64, "scales"), (8, 2, 64, 40, 0, "plain"), (4, 2, 80, 9, 4, False)]
+           (16, 4, 128, 50, 64, "scales"), (8, 2, 64, 40, 0, "plain"), (4, 2, 80, 9, 4, False),
+           (32, 8, 128, 520, 0, False), (32, 8, 128, 530, 3, "scales")]
 
 
 @pytest.mark.parametrize("H,KV,D,N,start,i8", PREFILL)
