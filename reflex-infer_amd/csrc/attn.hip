@@ -641,24 +641,32 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
     lds_sync();
     auto compute_tile = [&](int it, int b) {
         const int p0 = it * kAttnTile;
-        // S^T for the 4 sub-tiles of 16 positions.
+        // S^T for the 4 sub-tiles of 16 positions; the causal mask only on
+        // tiles that reach past the block's first token (uniform: every
+        // other tile is visible to all of the workgroup's rows).
         float sv[4][4];
+        auto scores = [&](bool mask) {
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int st = 0; st < 4; ++st) {
+                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int ks = 0; ks < HD / 32; ++ks) {
-                const u32x4 a = *reinterpret_cast<const u32x4 *>(
-                    &kt[b][(16 * st + r) * KROW + 32 * ks + 8 * g]);
-                acc = mfma<RXQ4_DTYPE_F16>(a, qf[ks], acc);
+                for (int ks = 0; ks < HD / 32; ++ks) {
+                    const u32x4 a = *reinterpret_cast<const u32x4 *>(
+                        &kt[b][(16 * st + r) * KROW + 32 * ks + 8 * g]);
+                    acc = mfma<RXQ4_DTYPE_F16>(a, qf[ks], acc);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int pp = 16 * st + 4 * g + i;
+                    const float s = acc[i] * sl2 * (I8 ? ksc[b][pp] : 1.0f);
+                    sv[st][i] = !mask || p0 + pp <= qpos ? s : -INFINITY;
+                }
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int pp = 16 * st + 4 * g + i;
-                const float s = acc[i] * sl2 * (I8 ? ksc[b][pp] : 1.0f);
-                sv[st][i] = p0 + pp <= qpos ? s : -INFINITY;
-            }
-        }
+        };
+        if (p0 + kAttnTile - 1 <= start + tb * TPB)
+            scores(false);
+        else
+            scores(true);
         float mx = -INFINITY;
 #pragma unroll
         for (int st = 0; st < 4; ++st)
@@ -669,14 +677,17 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
         const float m_new = fmaxf(m, mx);
         const bool live = m_new != -INFINITY;  // something visible so far
         const float corr = live ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+        // masked scores are -inf and exp2(-inf) = 0; rows with nothing
+        // visible yet subtract 0 instead of -inf
+        const float m_use = live ? m_new : 0.0f;
         float sum = 0.0f;
         uint32_t ph[2][4], pl[2][4];  // P^T hi / lo operands per 32-position k step
 #pragma unroll
         for (int st = 0; st < 4; ++st)
 #pragma unroll
             for (int i = 0; i < 4; i += 2) {
-                float e0 = live && sv[st][i] != -INFINITY ? __builtin_amdgcn_exp2f(sv[st][i] - m_new) : 0.0f;
-                float e1 = live && sv[st][i + 1] != -INFINITY ? __builtin_amdgcn_exp2f(sv[st][i + 1] - m_new) : 0.0f;
+                float e0 = __builtin_amdgcn_exp2f(sv[st][i] - m_use);
+                float e1 = __builtin_amdgcn_exp2f(sv[st][i + 1] - m_use);
                 sum += e0;
                 sum += e1;
                 if (I8) {
