@@ -522,41 +522,62 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
         u32x4 vr[TRV ? NST : 1];    // V chunks (TRV)
         float ks, vs;
     };
+    // Byte offsets of the thread's staging loads within a tile (row p - p0
+    // of the tile at (p - p0) * row_stride): the loads go through buffer
+    // resources based at the tile's first row and bounded at pos_end, so
+    // rows past the block's last visible position read zeros (their
+    // scores are masked) and no 64-bit address is formed per load.
+    int koff[NST], voff[TRV ? 1 : NSV][4];
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+        const int id = tid + 256 * j;
+        koff[j] = (int)((id / KCH) * row_stride) + (id % KCH) * 8 * esz;
+    }
+#pragma unroll
+    for (int j = 0; j < (TRV ? 0 : NSV); ++j) {
+        const int id = min(tid + 256 * j, NVU - 1);  // threads past the units reload the last
+        const int q4 = id % (kAttnTile / 4), vc = id / (kAttnTile / 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) voff[j][e] = (int)((4 * q4 + e) * row_stride) + vc * 8 * esz;
+    }
     auto load_tile = [&](int p0, Stage &S) {
+        // past the last tile (clamped prefetches that are never used): no rows
+        // (the values are wave-uniform; readfirstlane keeps the descriptors
+        // in scalar registers instead of a per-lane waterfall loop)
+        const int bytes = __builtin_amdgcn_readfirstlane(
+            (int)(max(0, min(pos_end - p0, kAttnTile)) * row_stride));
+        const int64_t tile_off = (int64_t)p0 * row_stride;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)tile_off);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(tile_off >> 32));
+        const int64_t toff = (int64_t)(((uint64_t)hi << 32) | lo);
+        const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb + toff, bytes);
+        const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb + toff, bytes);
 #pragma unroll
         for (int j = 0; j < NST; ++j) {
-            const int id = tid + 256 * j;
-            const int kpos = min(p0 + id / KCH, pos_end - 1), kc = id % KCH;
-            const uint8_t *krow = kb + kpos * row_stride;
             if (I8) {
-                const u32x2 a = reinterpret_cast<const u32x2 *>(krow)[kc];
+                const u32x2 a = buffer_load8(krs, koff[j]);
                 S.k[j] = u32x4{a.x, a.y, 0u, 0u};
             } else {
-                S.k[j] = reinterpret_cast<const u32x4 *>(krow)[kc];
+                S.k[j] = buffer_load16(krs, koff[j]);
             }
             if constexpr (TRV) {
-                const uint8_t *vrow = vb + kpos * row_stride;
                 if (I8) {
-                    const u32x2 b = reinterpret_cast<const u32x2 *>(vrow)[kc];
+                    const u32x2 b = buffer_load8(vrs, koff[j]);
                     S.vr[j] = u32x4{b.x, b.y, 0u, 0u};
                 } else {
-                    S.vr[j] = reinterpret_cast<const u32x4 *>(vrow)[kc];
+                    S.vr[j] = buffer_load16(vrs, koff[j]);
                 }
             }
         }
 #pragma unroll
         for (int j = 0; j < (TRV ? 0 : NSV); ++j) {
-            const int id = min(tid + 256 * j, NVU - 1);  // threads past the units reload the last
-            const int q4 = id % (kAttnTile / 4), vc = id / (kAttnTile / 4);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int vpos = min(p0 + 4 * q4 + e, pos_end - 1);
-                const uint8_t *vrow = vb + vpos * row_stride;
                 if (I8) {
-                    const u32x2 b = reinterpret_cast<const u32x2 *>(vrow)[vc];
+                    const u32x2 b = buffer_load8(vrs, voff[j][e]);
                     S.v[j][e] = u32x4{b.x, b.y, 0u, 0u};
                 } else {
-                    S.v[j][e] = reinterpret_cast<const u32x4 *>(vrow)[vc];
+                    S.v[j][e] = buffer_load16(vrs, voff[j][e]);
                 }
             }
         }
@@ -695,8 +716,14 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
                     e1 *= vsc[b][16 * st + 4 * g + i + 1];
                 }
                 const uint32_t hi = pack2<RXQ4_DTYPE_F16>(e0, e1);
-                const f16x2 hv = __builtin_bit_cast(f16x2, hi);
-                const uint32_t lo = pack2<RXQ4_DTYPE_F16>(e0 - (float)hv[0], e1 - (float)hv[1]);
+                // lo = RNE_f16(e - f32(hi)): e - f32(hi) is exact in fp32,
+                // so one fma_mix per half (e * 1 - hi, rounded once to fp16)
+                // gives what fp32 subtraction and conversion give
+                uint32_t lo;
+                asm volatile("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]"
+                             : "=v"(lo) : "v"(e0), "v"(hi));
+                asm volatile("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+                             : "+v"(lo) : "v"(e1), "v"(hi));
                 // k order of lane group g in step ks2: sub-tile 2 ks2 then 2 ks2 + 1
                 ph[st >> 1][2 * (st & 1) + (i >> 1)] = hi;
                 pl[st >> 1][2 * (st & 1) + (i >> 1)] = lo;
