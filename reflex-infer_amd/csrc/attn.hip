@@ -34,6 +34,7 @@
 namespace rxq4 {
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kAttnTile = 64;
 constexpr int kAttnMaxHeads = 8;   // query heads per workgroup
@@ -812,6 +813,238 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode on the matrix cores (one token, head_dim 64 / 128, GQA group <= 16).
+// A workgroup takes one KV head, all its query heads (the columns of a 16x16
+// MFMA tile; columns past the group multiply zero q) and one chunk of
+// positions.  Wave w takes positions 16w .. 16w+15 of every 64-position tile
+// of the chunk with its own online softmax; the four waves merge at the end.
+//   S^T = K . Q^T   v_mfma_f32_16x16x32_f16: src0 = 16 positions x 32 dims of
+//                   K straight from memory (16 bytes a lane), src1 = Q^T;
+//                   lane l gets positions 4(l/16) + i of head l%16;
+//   softmax         per head (lane column l%16), exp2 of log2e-scaled scores;
+//   O^T += V^T.P^T  v_mfma_f32_16x16x16_f16: src0 = 16 dims x 16 positions of
+//                   V^T by one ds_read_tr16_b64 of the wave's 16 V rows
+//                   (staged in its own LDS rows), src1 = P^T as the score
+//                   registers hold it (k = positions 4(l/16) + i); P as fp16
+//                   hi + lo parts, as in the prefill kernel.
+// The loads of up to four tiles go out before their arithmetic (one memory
+// round trip per workgroup for chunks of up to 256 positions); they go
+// through buffer resources based at each tile and bounded at the chunk's
+// end, so positions past it read zeros (their scores are masked).  Partials
+// use the VALU kernel's workspace format (o unnormalised, m in natural-log
+// units, l) for attn_combine_kernel, or the output directly when the chunk
+// is the whole sequence.
+template <int HD, bool I8>
+__global__ __launch_bounds__(256) void attn_decode_mfma(AttnParams p) {
+    constexpr int KS = HD / 32;        // k-steps of the scores
+    constexpr int DT = HD / 16;        // 16-dim tiles of O
+    constexpr int VROW = HD + 16;      // LDS V row (fp16), padded
+    constexpr int CH = HD / 8;         // 8-dim chunks per V row
+    constexpr int NV = 16 * CH / 64;   // V chunks per lane and tile
+    constexpr int NB = 4;              // tiles whose loads are in flight together
+    constexpr int esz = I8 ? 1 : 2;
+    constexpr int NM = DT * 4 + 2;     // merge values per lane: O, m, l
+    __shared__ __attribute__((aligned(16))) uint16_t vl[4][16 * VROW];
+    __shared__ float mg[4][NM][64];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int c = blockIdx.x % p.n_chunks;
+    const int kvh = blockIdx.x / p.n_chunks;
+    const int h0 = kvh * p.group;
+    const int beg = c * p.chunk;
+    const int end = min(p.seq0, beg + p.chunk);
+    const int64_t row_stride = (int64_t)p.n_kv * HD * esz;
+    const uint8_t *kb = static_cast<const uint8_t *>(p.k) + (int64_t)kvh * HD * esz;
+    const uint8_t *vb = static_cast<const uint8_t *>(p.v) + (int64_t)kvh * HD * esz;
+    const float *ksp = p.ks ? p.ks + kvh : &g_attn_one;
+    const float *vsp = p.vs ? p.vs + kvh : &g_attn_one;
+    const int s_stride = p.ks ? p.n_kv : 0, v_stride = p.vs ? p.n_kv : 0;
+    const float sl2 = p.scale * 1.4426950408889634f;  // scores in log2 units
+
+    // Q^T: column r = head h0 + r (zero past the group), dims 32 ks + 8 g .. + 7.
+    u32x4 qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        qf[ks] = r < p.group ? *reinterpret_cast<const u32x4 *>(p.q + (int64_t)(h0 + r) * HD + 32 * ks + 8 * g)
+                             : u32x4{0u, 0u, 0u, 0u};
+    // Byte offsets within a tile: the K fragment (position 16 w + r, dims
+    // 32 ks + 8 g) and the lane's V chunks (row id / CH, chunk id % CH).
+    const int kfo = (int)((16 * w + r) * row_stride) + 8 * g * esz;
+    int vfo[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int id = lane + 64 * j;
+        vfo[j] = (int)((16 * w + id / CH) * row_stride) + (id % CH) * 8 * esz;
+    }
+    // 8 int8 (bytes of .x, .y) as 8 fp16 (exact).
+    auto i8_to_f16 = [](u32x2 v) {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t wd = e < 2 ? v.x : v.y;
+            const int sh = 16 * (e & 1);
+            o[e] = pack2<RXQ4_DTYPE_F16>((float)(int8_t)(uint8_t)(wd >> sh),
+                                         (float)(int8_t)(uint8_t)(wd >> (sh + 8)));
+        }
+        return u32x4{o[0], o[1], o[2], o[3]};
+    };
+
+    f32x4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    const int n_tiles = (end - beg + kAttnTile - 1) / kAttnTile;  // 0 for an empty sequence
+
+    for (int j0 = 0; j0 < n_tiles; j0 += NB) {
+        u32x4 kf[NB][KS], vr[NB][NV];
+        float ksc[NB][4], vsc[NB][4];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int p0 = beg + kAttnTile * (j0 + b);
+            // tile base and bound as wave-uniform values (scalar descriptors)
+            const int bytes = __builtin_amdgcn_readfirstlane(
+                (int)(max(0, min(end - p0, kAttnTile)) * row_stride));
+            const int64_t toff = (int64_t)p0 * row_stride;
+            const uint32_t tlo = __builtin_amdgcn_readfirstlane((uint32_t)toff);
+            const uint32_t thi = __builtin_amdgcn_readfirstlane((uint32_t)(toff >> 32));
+            const int64_t to = (int64_t)(((uint64_t)thi << 32) | tlo);
+            const __amdgpu_buffer_rsrc_t krs = make_rsrc(kb + to, bytes);
+            const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vb + to, bytes);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                kf[b][ks] = I8 ? i8_to_f16(buffer_load8(krs, kfo + 32 * ks))
+                               : buffer_load16(krs, kfo + 64 * ks);
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                vr[b][j] = I8 ? i8_to_f16(buffer_load8(vrs, vfo[j])) : buffer_load16(vrs, vfo[j]);
+            if (I8) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int pos = min(p0 + 16 * w + 4 * g + i, end - 1);
+                    ksc[b][i] = ksp[(int64_t)pos * s_stride];
+                    vsc[b][i] = vsp[(int64_t)pos * v_stride];
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (j0 + b >= n_tiles) break;  // uniform
+            const int p0 = beg + kAttnTile * (j0 + b);
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) acc = mfma<RXQ4_DTYPE_F16>(kf[b][ks], qf[ks], acc);
+            float sv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s = acc[i] * sl2 * (I8 ? ksc[b][i] : 1.0f);
+                sv[i] = p0 + 16 * w + 4 * g + i < end ? s : -INFINITY;
+            }
+            float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m, mx);
+            const bool live = m_new != -INFINITY;
+            const float corr = live ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
+            const float m_use = live ? m_new : 0.0f;  // masked scores are -inf: exp2 gives 0
+            float e[4], sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                e[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
+                sum += e[i];
+                if (I8) e[i] *= vsc[b][i];
+            }
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            l = l * corr + sum;
+            m = m_new;
+            // P^T hi / lo (lo = RNE_f16(e - f32(hi)), exact difference, one rounding)
+            const uint32_t h01 = pack2<RXQ4_DTYPE_F16>(e[0], e[1]);
+            const uint32_t h23 = pack2<RXQ4_DTYPE_F16>(e[2], e[3]);
+            uint32_t l01, l23;
+            asm volatile("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(l01) : "v"(e[0]), "v"(h01));
+            asm volatile("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+                         : "+v"(l01) : "v"(e[1]), "v"(h01));
+            asm volatile("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(l23) : "v"(e[2]), "v"(h23));
+            asm volatile("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+                         : "+v"(l23) : "v"(e[3]), "v"(h23));
+            const f16x4 ph = __builtin_bit_cast(f16x4, u32x2{h01, h23});
+            const f16x4 pl = __builtin_bit_cast(f16x4, u32x2{l01, l23});
+            // the wave's V rows of this tile into its LDS rows (the wave's
+            // own earlier reads of them are ahead in its LDS queue)
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int id = lane + 64 * j;
+                *reinterpret_cast<u32x4 *>(&vl[w][(id / CH) * VROW + 8 * (id % CH)]) = vr[b][j];
+            }
+            // O^T = corr O^T + V^T . P^T; lane r of group g supplies dims
+            // 16 dt + 4 (r & 3) .. + 3 of position 4 g + r / 4 and receives
+            // dim 16 dt + r of positions 4 g .. 4 g + 3
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const f16x4 a = __builtin_bit_cast(
+                    f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16 *)
+                                                                   &vl[w][(4 * g + (r >> 2)) * VROW + 16 * dt + 4 * (r & 3)]));
+                o[dt] *= corr;
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pl, o[dt], 0, 0, 0);
+            }
+        }
+    }
+
+    // Merge the four waves: lane l of every wave holds head r, dims
+    // 16 dt + 4 g + i; wave w merges dims of tiles dt = w, w + 4, ...
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mg[w][4 * dt + i][lane] = o[dt][i];
+    mg[w][NM - 2][lane] = m;
+    mg[w][NM - 1][lane] = l;
+    __syncthreads();
+    float mw[4], M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        mw[v] = mg[v][NM - 2][lane];
+        M = fmaxf(M, mw[v]);
+    }
+    float cw[4], L = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        cw[v] = M != -INFINITY ? __builtin_amdgcn_exp2f(mw[v] - M) : 0.0f;
+        L += mg[v][NM - 1][lane] * cw[v];
+    }
+    const bool col_ok = r < p.group;
+    const int h = h0 + r;
+    float *wp = p.ws + ((int64_t)h * p.n_chunks + c) * (HD + 2);
+#pragma unroll
+    for (int dt = w; dt < DT; dt += 4) {
+        float ov[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float s = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) s += mg[v][4 * dt + i][lane] * cw[v];
+            ov[i] = s;
+        }
+        if (!col_ok) continue;
+        const int d = 16 * dt + 4 * g;
+        if (p.n_chunks == 1) {
+            const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+            const uint32_t a = pack2<RXQ4_DTYPE_F16>(ov[0] * inv, ov[1] * inv);
+            const uint32_t b = pack2<RXQ4_DTYPE_F16>(ov[2] * inv, ov[3] * inv);
+            *reinterpret_cast<u32x2 *>(p.out + (int64_t)h * HD + d) = u32x2{a, b};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wp[d + i] = ov[i];
+        }
+    }
+    if (p.n_chunks > 1 && col_ok && w == 0 && g == 0) {
+        wp[HD] = M * 0.6931471805599453f;  // natural-log units, as the VALU kernel's
+        wp[HD + 1] = L;
+    }
+}
+
 template <int HD, bool I8, int G>
 static void launch_prefill_g(unsigned grid, int hb, const AttnParams &p, int start, int n_tok,
                              hipStream_t st) {
@@ -877,7 +1110,11 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
     p.seq0 = seq0;
     p.scale = scale;
     p.kv_int8 = kv_int8;
-    const int units = n_kv * p.n_hg;
+    // decode on the matrix cores: one workgroup per KV head takes all of its
+    // query heads (the 16 columns of an MFMA tile)
+    const bool mfma_decode = n_tok == 1 && (head_dim == 64 || head_dim == 128) &&
+                             p.group <= 16 && tuning().attn_mfma;
+    const int units = mfma_decode ? n_kv : n_kv * p.n_hg;
     p.n_chunks = 1;
     p.chunk = seq0 + n_tok;  // whole sequence
     if (n_tok == 1 && seq0 > kAttnTile) {
@@ -913,6 +1150,19 @@ hipError_t launch_attention(uint16_t *out, const uint16_t *q, const void *k, con
             if (kv_int8) launch_prefill_hd<128, true>(p, hb, start, n_tok, st);
             else launch_prefill_hd<128, false>(p, hb, start, n_tok, st);
         }
+        return hipGetLastError();
+    }
+    if (mfma_decode) {
+        const unsigned grid = (unsigned)(n_kv * p.n_chunks);
+        if (head_dim == 64) {
+            if (kv_int8) attn_decode_mfma<64, true><<<grid, 256, 0, st>>>(p);
+            else attn_decode_mfma<64, false><<<grid, 256, 0, st>>>(p);
+        } else {
+            if (kv_int8) attn_decode_mfma<128, true><<<grid, 256, 0, st>>>(p);
+            else attn_decode_mfma<128, false><<<grid, 256, 0, st>>>(p);
+        }
+        if (p.n_chunks > 1)
+            attn_combine_kernel<<<n_heads * ((head_dim + 63) / 64), 256, 0, st>>>(p);
         return hipGetLastError();
     }
     if (n_tok > 65535) return hipErrorInvalidValue;  // grid.y
