@@ -434,41 +434,40 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 // give one wave per SIMD: 1024 waves at 512 tokens x 32 heads); at the end
 // group 1 hands its (m, l, O) to group 0 through LDS, which merges the two
 // online softmaxes and writes the rows.
-// Per 64-position tile, staged in LDS with the next tile's global loads in
-// flight during this tile's arithmetic (K row-major; V row-major with two
-// groups, V^T with one, see TRV below):
+// Per 64-position tile, staged in LDS (K and V row-major, 16-byte writes)
+// with the next tile's global loads in flight during this tile's arithmetic:
 //   S^T = K . Q^T   v_mfma_f32_16x16x32_f16: src0 = 16 positions x 32 dims
 //                   of K (LDS), src1 = Q^T (registers); lane l ends up with
 //                   positions 4 (l/16) + i of query row l % 16;
 //   online softmax  per query row (lane l % 16): the four lane groups
 //                   combine with two shuffles; exp2 of log2e-scaled scores;
 //   O^T += V^T . P^T the same MFMA with src0 = 16 dims x 32 positions of V^T
-//                   (LDS: two 8-byte reads of V^T, or two ds_read_tr16_b64
-//                   of the row-major V, each a 4 x 16 block transposed
-//                   across a 16-lane group) and src1 = P^T straight from the
-//                   score registers
+//                   (two ds_read_tr16_b64 of the row-major V, each a 4 x 16
+//                   block transposed across a 16-lane group) and src1 = P^T
+//                   straight from the score registers
 //                   (the k order of a lane group is its positions
 //                   {4g + i, 16 + 4g + i}, in both operands).  P is split
 //                   into fp16 hi + lo parts (two MFMAs), so the products
 //                   keep ~22 bits of the fp32 probabilities.
 // Causal: query row (t, h) sees positions [0, start + t]; rows of a tile
 // past that get probability 0 (rows with nothing visible yet keep m = -inf).
+// Launch bounds: two resident workgroups of the one-group form per CU (LDS
+// allows two), which caps a wave at 256 registers; uncapped, the compiler
+// spread the one-group kernel over AGPRs with ~320 accvgpr moves per two
+// tiles (2048 tokens 129 -> 119 us with the cap).
 template <int HD, int HB, bool I8, int G>
-__global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int start, int n_tok) {
+__global__ __launch_bounds__(256 * G, 2 / G) void attn_prefill_mfma(AttnParams p, int start, int n_tok) {
     constexpr int TPW = 16 / HB;       // tokens per wave
     constexpr int TPB = 4 * TPW;       // tokens per workgroup
-    // V staging: with two groups (the 512-token case) V is stored row-major
-    // with 16-byte writes and read transposed (ds_read_tr16_b64); with one,
-    // V^T is written by the threads (8-byte writes of 4 positions of one
-    // dim) and read with plain 8-byte reads.  Measured (32 / 8 heads,
-    // head_dim 128): 512 tokens 18.45 -> 17.2 us with the transposing
-    // reads, 2048 tokens 131 -> 139 us, so one group keeps V^T.
-    constexpr bool TRV = G == 2;
+    // V is stored row-major with 16-byte writes and read transposed
+    // (ds_read_tr16_b64); threads writing V^T with 8-byte writes instead
+    // measured slower (512 tokens 18.45 against 17.2 us, 2048 tokens 119
+    // against 111 us).
     constexpr int KROW = HD + 8;       // LDS K row (fp16), padded: 16 rows of a fragment read hit 64 banks
-    constexpr int VROW = TRV ? HD + 16 : kAttnTile + 4;  // LDS V (TRV) or V^T row (fp16), padded
+    constexpr int VROW = HD + 16;      // LDS V row (fp16), padded: 8 rows of a transposed read hit 64 banks
     constexpr int KCH = HD / 8;        // 8-dim chunks per row
     constexpr int NST = kAttnTile * KCH / 256;  // staged chunks per thread (K and V each)
-    constexpr int VSZ = TRV ? kAttnTile * VROW : HD * VROW;
+    constexpr int VSZ = kAttnTile * VROW;
     __shared__ __attribute__((aligned(16))) uint16_t ktg[G][2][kAttnTile * KROW];
     __shared__ __attribute__((aligned(16))) uint16_t vtg[G][2][VSZ];
     __shared__ float kscg[G][2][kAttnTile], vscg[G][2][kAttnTile];
@@ -511,16 +510,10 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
     }
 
     // Staging registers, a ring of two tiles (tile j in set j & 1, loaded
-    // two iterations before it is used): K chunks row-major (16 lanes per
-    // row: coalesced), V the same with TRV, else in units of 4 consecutive
-    // positions x 8 dims, so the transposed LDS writes are 8 bytes (4
-    // positions of one dim).
-    constexpr int NVU = kAttnTile / 4 * KCH;          // V units per tile
-    constexpr int NSV = (NVU + 255) / 256;            // V units per thread
+    // two iterations before it is used): K and V chunks row-major (16 lanes
+    // per row: coalesced).
     struct Stage {
-        u32x4 k[NST];
-        u32x4 v[TRV ? 1 : NSV][4];  // V units (not TRV)
-        u32x4 vr[TRV ? NST : 1];    // V chunks (TRV)
+        u32x4 k[NST], vr[NST];
         float ks, vs;
     };
     // Byte offsets of the thread's staging loads within a tile (row p - p0
@@ -528,18 +521,11 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
     // resources based at the tile's first row and bounded at pos_end, so
     // rows past the block's last visible position read zeros (their
     // scores are masked) and no 64-bit address is formed per load.
-    int koff[NST], voff[TRV ? 1 : NSV][4];
+    int koff[NST];
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
         const int id = tid + 256 * j;
         koff[j] = (int)((id / KCH) * row_stride) + (id % KCH) * 8 * esz;
-    }
-#pragma unroll
-    for (int j = 0; j < (TRV ? 0 : NSV); ++j) {
-        const int id = min(tid + 256 * j, NVU - 1);  // threads past the units reload the last
-        const int q4 = id % (kAttnTile / 4), vc = id / (kAttnTile / 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) voff[j][e] = (int)((4 * q4 + e) * row_stride) + vc * 8 * esz;
     }
     auto load_tile = [&](int p0, Stage &S) {
         // past the last tile (clamped prefetches that are never used): no rows
@@ -561,25 +547,11 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
             } else {
                 S.k[j] = buffer_load16(krs, koff[j]);
             }
-            if constexpr (TRV) {
-                if (I8) {
-                    const u32x2 b = buffer_load8(vrs, koff[j]);
-                    S.vr[j] = u32x4{b.x, b.y, 0u, 0u};
-                } else {
-                    S.vr[j] = buffer_load16(vrs, koff[j]);
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < (TRV ? 0 : NSV); ++j) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if (I8) {
-                    const u32x2 b = buffer_load8(vrs, voff[j][e]);
-                    S.v[j][e] = u32x4{b.x, b.y, 0u, 0u};
-                } else {
-                    S.v[j][e] = buffer_load16(vrs, voff[j][e]);
-                }
+            if (I8) {
+                const u32x2 b = buffer_load8(vrs, koff[j]);
+                S.vr[j] = u32x4{b.x, b.y, 0u, 0u};
+            } else {
+                S.vr[j] = buffer_load16(vrs, koff[j]);
             }
         }
         if (I8 && tid < kAttnTile) {
@@ -605,35 +577,9 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
         for (int j = 0; j < NST; ++j) {
             const int id = tid + 256 * j;
             const u32x4 kv = I8 ? i8_to_f16(S.k[j]) : S.k[j];
+            const u32x4 vv = I8 ? i8_to_f16(S.vr[j]) : S.vr[j];
             *reinterpret_cast<u32x4 *>(&kt[b][(id / KCH) * KROW + 8 * (id % KCH)]) = kv;
-            if constexpr (TRV) {
-                const u32x4 vv = I8 ? i8_to_f16(S.vr[j]) : S.vr[j];
-                *reinterpret_cast<u32x4 *>(&vt[b][(id / KCH) * VROW + 8 * (id % KCH)]) = vv;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < (TRV ? 0 : NSV); ++j) {
-            const int id = tid + 256 * j;
-            if (id < NVU) {
-                const int q4 = id % (kAttnTile / 4), d0 = 8 * (id / (kAttnTile / 4));
-                uint32_t w[4][4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const u32x4 vv = I8 ? i8_to_f16(S.v[j][e]) : S.v[j][e];
-                    w[e][0] = vv.x; w[e][1] = vv.y; w[e][2] = vv.z; w[e][3] = vv.w;
-                }
-                // dim d0 + 2c + hh: halves hh of word c of positions 4 q4 .. + 3
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const int sh = 16 * hh;
-                        const uint32_t lo = ((w[0][c] >> sh) & 0xFFFFu) | (((w[1][c] >> sh) & 0xFFFFu) << 16);
-                        const uint32_t hi = ((w[2][c] >> sh) & 0xFFFFu) | (((w[3][c] >> sh) & 0xFFFFu) << 16);
-                        *reinterpret_cast<u32x2 *>(&vt[b][(d0 + 2 * c + hh) * VROW + 4 * q4]) =
-                            u32x2{lo, hi};
-                    }
-            }
+            *reinterpret_cast<u32x4 *>(&vt[b][(id / KCH) * VROW + 8 * (id % KCH)]) = vv;
         }
         if (I8 && tid < kAttnTile) {
             ksc[b][tid] = S.ks;
@@ -741,23 +687,16 @@ __global__ __launch_bounds__(256 * G) void attn_prefill_mfma(AttnParams p, int s
             for (int ks2 = 0; ks2 < 2; ++ks2) {
                 // V^T operand: dim 16 dt + r, positions {32 ks2 + 4 g + i,
                 // 32 ks2 + 16 + 4 g + i}
-                u32x2 v0, v1;
-                if constexpr (TRV) {
-                    // lane 4e + c of a 16-lane group supplies dims
-                    // 16 dt + 4c .. +3 of position 32 ks2 + 4 g + e; lane r
-                    // receives dim 16 dt + r of the four positions
-                    const uint16_t *vp =
-                        &vt[b][(32 * ks2 + 4 * g + (r >> 2)) * VROW + 16 * dt + 4 * (r & 3)];
-                    v0 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                       (__attribute__((address_space(3))) v4i16 *)vp));
-                    v1 = __builtin_bit_cast(
-                        u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                   (__attribute__((address_space(3))) v4i16 *)(vp + 16 * VROW)));
-                } else {
-                    const uint16_t *vrow = &vt[b][(16 * dt + r) * VROW + 32 * ks2 + 4 * g];
-                    v0 = *reinterpret_cast<const u32x2 *>(vrow);
-                    v1 = *reinterpret_cast<const u32x2 *>(vrow + 16);
-                }
+                // lane 4e + c of a 16-lane group supplies dims 16 dt + 4c .. +3
+                // of position 32 ks2 + 4 g + e; lane r receives dim 16 dt + r
+                // of the four positions
+                const uint16_t *vp =
+                    &vt[b][(32 * ks2 + 4 * g + (r >> 2)) * VROW + 16 * dt + 4 * (r & 3)];
+                const u32x2 v0 = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                               (__attribute__((address_space(3))) v4i16 *)vp));
+                const u32x2 v1 = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                               (__attribute__((address_space(3))) v4i16 *)(vp + 16 * VROW)));
                 const u32x4 a = u32x4{v0.x, v0.y, v1.x, v1.y};
                 o[dt] = mfma<RXQ4_DTYPE_F16>(a, u32x4{ph[ks2][0], ph[ks2][1], ph[ks2][2], ph[ks2][3]}, o[dt]);
                 o[dt] = mfma<RXQ4_DTYPE_F16>(a, u32x4{pl[ks2][0], pl[ks2][1], pl[ks2][2], pl[ks2][3]}, o[dt]);
