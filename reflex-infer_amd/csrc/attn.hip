@@ -774,8 +774,11 @@ __global__ __launch_bounds__(256 * G, 2 / G) void attn_prefill_mfma(AttnParams p
 // use the VALU kernel's workspace format (o unnormalised, m in natural-log
 // units, l) for attn_combine_kernel, or the output directly when the chunk
 // is the whole sequence.
+// Launch bounds: at least two workgroups per CU, i.e. at most 256 registers
+// a wave; uncapped the compiler moved values through AGPRs (336 accvgpr
+// moves in the head_dim 128 kernel).
 template <int HD, bool I8>
-__global__ __launch_bounds__(256) void attn_decode_mfma(AttnParams p) {
+__global__ __launch_bounds__(256, 2) void attn_decode_mfma(AttnParams p) {
     constexpr int KS = HD / 32;        // k-steps of the scores
     constexpr int DT = HD / 16;        // 16-dim tiles of O
     constexpr int VROW = HD + 16;      // LDS V row (fp16), padded
