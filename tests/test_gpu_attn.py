@@ -67,12 +67,14 @@ def test_decode_fp16(H, KV, D, S):
     check(host16(out), ref64, ref32)
 
 
+# (n_heads, n_kv, head_dim): the matrix-core decode kernel at head_dim 128
+# (GQA 4) and 64 (GQA 8), and the VALU kernel at head_dim 80 (GQA 2)
+@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (16, 2, 64), (8, 4, 80)])
 @pytest.mark.parametrize("scales", [True, False])
 @pytest.mark.parametrize("S", [2000, 9000])
-def test_decode_int8(scales, S):
-    print(f"attention decode int8 S={S} scales={scales}", flush=True)
-    H, KV, D = 32, 8, 128
-    r = util.rng(910)
+def test_decode_int8(H, KV, D, scales, S):
+    print(f"attention decode int8 H={H} KV={KV} D={D} S={S} scales={scales}", flush=True)
+    r = util.rng(910 + D)
     q = f16(r.standard_normal(H * D))
     ki = r.integers(-127, 128, (S, KV, D)).astype(np.int8)
     vi = r.integers(-127, 128, (S, KV, D)).astype(np.int8)
