@@ -86,7 +86,8 @@ struct GemmParams {
     int M, N, K, nb;
     int row_tiles, tok_tiles, splits, sb_per_split;
     int total_units, units_per_xcd;
-    int tok_major;  // unit order (see gemm_kernel)
+    int tok_major;    // unit order (see gemm_kernel)
+    int big_per_xcd;  // gemm_mixed_kernel: whole areas per XCD
 };
 
 constexpr int kW8Rows = 32;                       // weight rows per wave
@@ -317,8 +318,17 @@ struct GemmFmt<14> {
     }
 };
 
+// LDS of one workgroup: the x ring, reused for the staged output tile.
+template <int TM>
+constexpr int gemm_lds_bytes() {
+    return TM * kOutPitch > kRing * TM * 128 ? TM * kOutPitch : kRing * TM * 128;
+}
+
+// One output tile: rows [256 * row_tile, +256) x tokens [TM * tok_tile, +TM)
+// over super-blocks [split * sb_per_split, +sb_per_split).
 template <int T, int XT, int YT, int TM>
-__global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
+__device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int split,
+                                          int row_tile, int tok_tile) {
     using F = GemmFmt<T>;
     // TM tokens per workgroup tile (128 or 256)
     constexpr int NT = TM / 32;      // 32-token fragments per wave
@@ -327,33 +337,6 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
     constexpr int kQLoads = F::kQLoads, kHLoads = F::kHLoads;
     constexpr int kLook = 6;         // B fragments are read kLook MFMAs before use
     constexpr int kBufBytes = TM * 128;                        // one stage of x
-    constexpr int kLdsBytes = TM * kOutPitch > kRing * kBufBytes ? TM * kOutPitch
-                                                                : kRing * kBufBytes;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
-
-    const int L = blockIdx.x;
-    const int V = (L % 8) * p.units_per_xcd + L / 8;  // consecutive units share an XCD
-    if (V >= p.total_units) return;
-    // Unit order.  Row-major, V = (row_tile * tok_tiles + tok_tile) * splits
-    // + split: an XCD holds all token tiles and splits of its row tiles, so
-    // it reads their weights once and every XCD reads all of x.
-    // Token-major, V = (tok_tile * splits + split) * row_tiles + row_tile:
-    // an XCD holds all row tiles of a few (token tile, split) pairs, so it
-    // reads only their part of x and the weights once per token tile.  The
-    // launcher takes the order with less L2 fill traffic (8 x-reads + the
-    // weights against x + one weight read per token tile).
-    int split, row_tile, tok_tile;
-    if (p.tok_major) {
-        row_tile = V % p.row_tiles;
-        const int r = V / p.row_tiles;
-        split = r % p.splits;
-        tok_tile = r / p.splits;
-    } else {
-        split = V % p.splits;
-        const int t = V / p.splits;
-        row_tile = t / p.tok_tiles;
-        tok_tile = t % p.tok_tiles;
-    }
     const int tile = row_tile * p.tok_tiles + tok_tile;
     const int sb0 = split * p.sb_per_split;
     const int nsb = min(p.nb, sb0 + p.sb_per_split) - sb0;
@@ -570,6 +553,71 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
                              acc[tf][4 * j + 3]},
                        vec_ok && valid == 4, valid);
         }
+}
+
+template <int T, int XT, int YT, int TM>
+__global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[gemm_lds_bytes<TM>()];
+    const int L = blockIdx.x;
+    const int V = (L % 8) * p.units_per_xcd + L / 8;  // consecutive units share an XCD
+    if (V >= p.total_units) return;
+    // Unit order.  Row-major, V = (row_tile * tok_tiles + tok_tile) * splits
+    // + split: an XCD holds all token tiles and splits of its row tiles, so
+    // it reads their weights once and every XCD reads all of x.
+    // Token-major, V = (tok_tile * splits + split) * row_tiles + row_tile:
+    // an XCD holds all row tiles of a few (token tile, split) pairs, so it
+    // reads only their part of x and the weights once per token tile.  The
+    // launcher takes the order with less L2 fill traffic (8 x-reads + the
+    // weights against x + one weight read per token tile).
+    int split, row_tile, tok_tile;
+    if (p.tok_major) {
+        row_tile = V % p.row_tiles;
+        const int r = V / p.row_tiles;
+        split = r % p.splits;
+        tok_tile = r / p.splits;
+    } else {
+        split = V % p.splits;
+        const int t = V / p.splits;
+        row_tile = t / p.tok_tiles;
+        tok_tile = t % p.tok_tiles;
+    }
+    gemm_tile<T, XT, YT, TM>(p, lds, split, row_tile, tok_tile);
+}
+
+// Mixed token tiles for GEMMs that fill the CUs between one and two times
+// with 256-token tiles.  The units are the 256-token tiles ("areas", no K
+// split), dealt to the XCDs in runs of units_per_xcd as in gemm_kernel.
+// Workgroup j of an XCD (block 8j + xcd) takes the XCD's area j whole while
+// j < big_per_xcd (one per CU: the first round), and the later areas as two
+// 128-token halves, which the CUs take as the whole tiles finish.  Every
+// output element sums the same products in the same order as either kernel
+// alone.
+template <int T, int XT, int YT>
+__global__ __launch_bounds__(512) void gemm_mixed_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[gemm_lds_bytes<256>()];
+    const int L = blockIdx.x;
+    const int xcd = L % 8, j = L / 8;
+    const int first = xcd * p.units_per_xcd;
+    const int end = min(p.total_units, first + p.units_per_xcd);
+    const bool whole = j < p.big_per_xcd;
+    const int u = whole ? j : p.big_per_xcd + ((j - p.big_per_xcd) >> 1);
+    const int V = first + u;
+    if (V >= end) return;
+    int row_tile, tok_tile;
+    if (p.tok_major) {
+        row_tile = V % p.row_tiles;
+        tok_tile = V / p.row_tiles;
+    } else {
+        row_tile = V / p.tok_tiles;
+        tok_tile = V % p.tok_tiles;
+    }
+    if (whole) {
+        gemm_tile<T, XT, YT, 256>(p, lds, 0, row_tile, tok_tile);
+    } else {
+        const int t128 = 2 * tok_tile + ((j - p.big_per_xcd) & 1);
+        if (t128 * 128 >= p.N) return;  // the second half of a partial last area
+        gemm_tile<T, XT, YT, 128>(p, lds, 0, row_tile, t128);
+    }
 }
 
 // Split-K reduction for gemm_kernel: block (tile, e), e = tf*4 + j, sums
@@ -964,27 +1012,84 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     return hipGetLastError();
 }
 
+// One round of 256-token tiles (one workgroup per CU) against one of
+// 128-token tiles: measured ~1.6x for twice the work ([11008 x 2048] on one
+// box: 54-60 us against 35-37 us).
+constexpr int kBigTileCost = 16, kHalfTileCost = 10;
+
+// Mixed token tiles (gemm_mixed_kernel): areas of 256 tokens dealt to the
+// XCDs, the first big_per_xcd of each run whole, the rest as 128-token
+// halves.  Q4_K/Q5_K only, no K split (it is taken with at least one
+// 128-token tile per CU).
+template <int T, int XT, int YT>
+static hipError_t launch_gemm_mixed(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
+                                   int K, int big_per_xcd, hipStream_t st) {
+    if ((int64_t)256 * K * 2 > 0x7FFFFFFF) return hipErrorInvalidValue;
+    GemmParams p{};
+    p.y = y;
+    p.w = w;
+    p.x = x;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.nb = K / 256;
+    p.row_tiles = (M + kRowsPerWg - 1) / kRowsPerWg;
+    p.tok_tiles = (N + 255) / 256;
+    p.splits = 1;
+    p.sb_per_split = p.nb;
+    p.total_units = p.row_tiles * p.tok_tiles;
+    p.units_per_xcd = (p.total_units + 7) / 8;
+    p.big_per_xcd = std::min(big_per_xcd, p.units_per_xcd);
+    const double x_bytes = 2.0 * N * K, w_bytes = (double)M * (K / 256) * GemmFmt<T>::kBytes;
+    p.tok_major = tuning().gemm_order ? tuning().gemm_order == 2
+                                      : x_bytes + p.tok_tiles * w_bytes < 8 * x_bytes + w_bytes;
+    const int per_xcd = p.big_per_xcd + 2 * (p.units_per_xcd - p.big_per_xcd);
+    gemm_mixed_kernel<T, XT, YT><<<8 * per_xcd, 512, 0, st>>>(p);
+    return hipGetLastError();
+}
+
 // Token tile.  256 tokens per workgroup halve the dequantisation per MFMA
-// (each wave's 32 dequantised rows feed 8 token fragments): measured, a
-// 256-token tile costs ~1.5x a 128-token one for twice the work.  It is
-// used when the GEMM fills the CUs several times over and needs fewer
-// launch waves that way (m = 4096 on [11008 x 2048]: 3 rounds of 688 tiles
-// instead of 6 of 1376); with fewer tiles than CUs the 128-token tile and
-// its K splits win (the 256-token partials double the split traffic).
-// Q6_K keeps 128 (its format needs more registers).
+// (each wave's 32 dequantised rows feed 8 token fragments) for ~1.6x the
+// time of a 128-token tile.  With at least one 128-token tile per CU the
+// launcher estimates, per XCD, the time of R rounds of whole 256-token
+// tiles followed by the remaining areas as 128-token halves (R = 0: the
+// 128-token kernel; every area whole: the 256-token kernel; else the mixed
+// kernel), and takes the fastest: m = 1024 on [11008 x 2048] (22 areas per
+// XCD of 32 CUs) one round of 256; m = 2048 (43 areas) one round of 256
+// and 22 halves against 3 rounds of 128 or 2 of 256; m = 4096 three rounds
+// of 256.  With fewer 128-token tiles than CUs the 128-token tile and its
+// K splits win (the 256-token partials double the split traffic).  Q6_K
+// keeps 128 (its format needs more registers).
 template <int T, int XT, int YT>
 static hipError_t launch_gemm_tm(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
                                  int K, hipStream_t st, const Scratch &sc) {
     int tm = tuning().gemm_tm;
+    int big = -1;  // whole areas per XCD for the mixed kernel
     if (tm != 128 && tm != 256) {
         const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+        const int c = std::max(1, cus / 8);  // CUs per XCD
         const int64_t rows = (M + kRowsPerWg - 1) / kRowsPerWg;
         const int64_t t128 = rows * ((N + 127) / 128), t256 = rows * ((N + 255) / 256);
-        const int64_t r128 = (t128 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
-        tm = (t128 >= cus && 3 * r256 < 2 * r128) ? 256 : 128;
+        tm = 128;
+        if (T != 14 && t128 >= cus) {
+            const int64_t a = (t256 + 7) / 8, u128 = (t128 + 7) / 8;  // per XCD
+            int64_t best = ((u128 + c - 1) / c) * kHalfTileCost;
+            for (int64_t r = 1; r <= (a + c - 1) / c; ++r) {
+                const int64_t halves = 2 * std::max<int64_t>(0, a - r * c);
+                const int64_t cost = r * kBigTileCost + (halves + c - 1) / c * kHalfTileCost;
+                if (cost < best) {
+                    best = cost;
+                    tm = 256;
+                    big = halves ? (int)(r * c) : -1;
+                }
+            }
+        }
     }
-    if constexpr (T != 14)
+    if (tuning().gemm_mixed > 0 && T != 14) big = tuning().gemm_mixed;
+    if constexpr (T != 14) {
+        if (big > 0) return launch_gemm_mixed<T, XT, YT>(y, w, x, M, N, K, big, st);
         if (tm == 256) return launch_gemm_t<T, XT, YT, 256>(y, w, x, M, N, K, st, sc);
+    }
     return launch_gemm_t<T, XT, YT, 128>(y, w, x, M, N, K, st, sc);
 }
 

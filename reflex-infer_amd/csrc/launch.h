@@ -140,6 +140,7 @@ struct Tuning {
     int multi_token_gemv = -1;  // 2..4 tokens on the multi-token GEMV: -1 measured crossover, 0 never, 1 always
     int gemm_tm = 0;
     int gemm_order = 0;
+    int gemm_mixed = 0;  // > 0: mixed token tiles with this many whole areas per XCD
     int tokens_waves = 0;
     int tokens_lds_split = 0;
 };

@@ -81,6 +81,7 @@ const Tuning &tuning() {
                              : env_pos("RXQ4_MULTI_TOKEN_GEMV") ? 1 : -1;
         r.gemm_tm = env_pos("RXQ4_GEMM_TM");
         r.gemm_order = env_pos("RXQ4_GEMM_ORDER");
+        r.gemm_mixed = env_pos("RXQ4_GEMM_MIXED");
         r.tokens_waves = env_pos("RXQ4_TOKENS_WAVES");
         r.tokens_lds_split = env_pos("RXQ4_TOKENS_LDS_SPLIT");
         return r;

@@ -477,6 +477,41 @@ def test_prefill_gemm_256_token_tile(t):
     assert util.rounded_ok(got, ref, "bf16").all()
 
 
+@pytest.mark.parametrize("t", [12, 13])
+def test_prefill_gemm_mixed_token_tiles(t):
+    """1472 tokens on [11008 x 2048]: 258 areas of 256 tokens, 33 on each of
+    seven XCDs of 32 CUs, so the launcher takes the mixed kernel (the 33rd
+    area of an XCD as two 128-token halves, one of them 64 tokens long).
+    Every output must equal, bit for bit, the 256-token kernel run on the
+    two token slices on their own (768 and 704 tokens: one round each, no K
+    split), and sampled rows must match the fp64 product of the kernel's
+    operands."""
+    M, N, K = 11008, 1472, 2048
+    print(f"mixed token tiles t={t} [{M}x{K}] m={N}", flush=True)
+    W = qweights(9100 + t, M, K, t)
+    g = torch.Generator(device="cuda").manual_seed(9101)
+    x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+    yb = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+    y32 = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    capi.gemm(yb, W, x, M, N, K, ggml_type=t)
+    capi.gemm(y32, W, x, M, N, K, ggml_type=t)
+    for a, b in ((0, 768), (768, N)):
+        sb = torch.empty((b - a, M), dtype=torch.bfloat16, device="cuda")
+        s32 = torch.empty((b - a, M), dtype=torch.float32, device="cuda")
+        capi.gemm(sb, W, x[a:b], M, b - a, K, ggml_type=t)
+        capi.gemm(s32, W, x[a:b], M, b - a, K, ggml_type=t)
+        assert torch.equal(yb[a:b].view(torch.int16), sb.view(torch.int16))
+        assert torch.equal(y32[a:b].view(torch.int32), s32.view(torch.int32))
+    rows = np.sort(util.rng(9102).choice(M, 64, replace=False))
+    Wn = sample_rows(W, rows)
+    wb = (orc.kq_dequant_f32(Wn, K, t) if t != 12 else orc.dequant_f32(Wn, K))
+    wb = orc.bits_bf16_to_f32(util.f32_to_bf16_bits(wb)).astype(np.float64).reshape(len(rows), K)
+    ref = x.float().cpu().numpy().astype(np.float64) @ wb.T
+    assert util.rel_err(y32.cpu().numpy()[:, rows], ref) <= util.TOL
+    got = yb.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows]
+    assert util.rounded_ok(got, ref, "bf16").all()
+
+
 # ------------------------- small batch with x in LDS: super-block counts
 @pytest.mark.parametrize("M,m,K", [(16448, 12, 2816), (16384, 5, 512), (22016, 16, 4096)])
 def test_small_batch_lds_kernel_block_counts(M, m, K):
