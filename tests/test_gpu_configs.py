@@ -512,6 +512,28 @@ def test_prefill_gemm_mixed_token_tiles(t):
     assert util.rounded_ok(got, ref, "bf16").all()
 
 
+def test_prefill_gemm_mixed_token_tiles_f16():
+    """The mixed kernel's fp16-activation, fp16-output form (Q4_K, 1472 tokens
+    on [11008 x 2048]): equal bit for bit to the 256-token kernel on the two
+    token slices, and sampled rows within one fp16 rounding of the fp64
+    product of fp16-rounded weights."""
+    M, N, K = 11008, 1472, 2048
+    print(f"mixed token tiles f16 [{M}x{K}] m={N}", flush=True)
+    W = qweights(9110, M, K)
+    x16 = util.x_f16(9111, (N, K))
+    x = dev(x16).view(torch.float16)
+    y = torch.empty((N, M), dtype=torch.float16, device="cuda")
+    capi.gemm(y, W, x, M, N, K, ggml_type=12)
+    for a, b in ((0, 768), (768, N)):
+        s = torch.empty((b - a, M), dtype=torch.float16, device="cuda")
+        capi.gemm(s, W, x[a:b], M, b - a, K, ggml_type=12)
+        assert torch.equal(y[a:b].view(torch.int16), s.view(torch.int16))
+    rows = np.sort(util.rng(9112).choice(M, 64, replace=False))
+    Wn = sample_rows(W, rows)
+    got = host16(y)[:, rows]
+    assert util.rounded_ok(got, orc.gemm_f64(Wn, K, f16(x16), "f16")).all()
+
+
 # ------------------------- small batch with x in LDS: super-block counts
 @pytest.mark.parametrize("M,m,K", [(16448, 12, 2816), (16384, 5, 512), (22016, 16, 4096)])
 def test_small_batch_lds_kernel_block_counts(M, m, K):
