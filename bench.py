@@ -124,6 +124,7 @@ LEGS = {
     "embed": (12, VOCAB, HIDDEN, 4096, "embed"),
     "gemm512_11008x2048": (12, FFN, HIDDEN, 512, "gemm"),
     "gemm512_2048x11008": (12, HIDDEN, FFN, 512, "gemm"),
+    "gemm2048_11008x2048": (12, FFN, HIDDEN, 2048, "gemm"),
     "gate_up_m8": (12, 2 * FFN, HIDDEN, 8, "tokens"),
     "gate_up_m16": (12, 2 * FFN, HIDDEN, 16, "tokens"),
     "down_m16": (12, HIDDEN, FFN, 16, "tokens"),
