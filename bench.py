@@ -48,6 +48,9 @@ Profiling entry points (no timing, for rocprofv3 counter passes):
                     copies (gate_up, down, lm_head, embed, the m=512 GEMM
                     shapes, small batch gate_up_m8 / gate_up_m16 / down_m16,
                     attn_prefill)
+  --leg NAME --graph  the same workload as 72 launches in a HIP graph,
+                    replayed 10 times; prints the per-launch time from HIP
+                    events (the figure the kernel trace is compared with)
   --calibrate-copy  a 256 MiB device copy, to scale FETCH_SIZE / WRITE_SIZE
 """
 from __future__ import annotations
@@ -132,7 +135,7 @@ LEGS = {
 }
 
 
-def run_leg(name: str) -> int:
+def run_leg(name: str, graph: bool = False) -> int:
     import numpy as np
     import torch
 
@@ -198,10 +201,43 @@ def run_leg(name: str) -> int:
             run = lambda i: capi.gemv_multi_f16(  # noqa: E731
                 [(y[:h], ws[i % n_copies][:h], h), (y[h:], ws[i % n_copies][h:], h)], x, K)
     torch.cuda.synchronize()
-    for i in range(launches):
-        run(i)
+    if not graph:
+        for i in range(launches):
+            run(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"leg": name, "launches": launches, "weight_copies": n_copies}), flush=True)
+        return 0
+    # --graph: 72 launches (distinct copies in rotation) captured in a HIP
+    # graph on a side stream and replayed 10 times between HIP events on that
+    # stream, as the bench's per-kernel figures are taken; the kernel trace
+    # of this same command is what profiles/ compares them with.
+    n_graph, reps = 72, 10
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(3):
+            run(i)
     torch.cuda.synchronize()
-    print(json.dumps({"leg": name, "launches": launches, "weight_copies": n_copies}), flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream, capture_error_mode="relaxed"):
+        for i in range(n_graph):
+            run(i)
+    with torch.cuda.stream(stream):
+        g.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / n_graph)
+    print(json.dumps({"leg": name, "graph_launches": n_graph, "replays": reps + 1,
+                      "weight_copies": n_copies, "us_per_launch_median": round(float(np.median(per)), 3),
+                      "us_per_launch_mean": round(float(np.mean(per)), 3),
+                      "us_per_launch_all": [round(v, 3) for v in per]}), flush=True)
     return 0
 
 
@@ -213,6 +249,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip LM head / embedding / GEMM")
     ap.add_argument("--eager", action="store_true", help="time eager launches, not a graph")
+    ap.add_argument("--graph", action="store_true",
+                    help="with --leg: replay the leg's launches as a HIP graph and print the "
+                         "per-launch time from HIP events")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--leg", choices=sorted(LEGS),
@@ -224,7 +263,7 @@ def parse():
 def main() -> int:
     args = parse()
     if args.leg:
-        return run_leg(args.leg)
+        return run_leg(args.leg, args.graph)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the Q4_K kernels run on one MI355X; sharding is design-only). "
@@ -459,6 +498,8 @@ def main() -> int:
                                      ctypes.c_int, ctypes.c_void_p]
     flib.rxq4_floor_read_runs.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                           ctypes.c_int, ctypes.c_void_p]
+    flib.rxq4_floor_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     floors = {}
     med, _ = per_launch(lambda i: flib.rxq4_floor_empty(sp), R)
     floors["empty_kernel_us"] = round(med, 3)
@@ -491,13 +532,25 @@ def main() -> int:
         floors[f"stream_read_{name}"] = {"bytes": nbytes, "us": round(us, 3),
                                          "GBps": round(nbytes / us / 1e3, 1), "kernel": best[2]}
         del bufs, sink
-    # Sustained read: one 2 GiB buffer, 32 KB runs (HBM, not the Infinity Cache).
+    # Sustained read ceiling: a persistent grid-stride read of one 2 GiB
+    # buffer (HBM, not the Infinity Cache), two batches of 16-byte loads in
+    # flight per lane, with and without the nontemporal bit; the best of a
+    # small sweep of grid sizes.  No GEMV is expected above it.
     big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
-    sink = torch.empty((2 << 30) // (32 << 10) // 4, dtype=torch.int32, device=dev)
-    med, _ = per_launch(lambda i: flib.rxq4_floor_read_runs(big.data_ptr(), 2 << 30,
-                                                             sink.data_ptr(), 32, sp), 3)
-    floors["stream_read_2GiB"] = {"bytes": 2 << 30, "us": round(med, 1),
-                                  "GBps": round((2 << 30) / med / 1e3, 1)}
+    big.fill_(1)
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+    sweep = {}
+    for nt in (0, 1):
+        for blocks in (256, 512, 1024):
+            med, _ = per_launch(lambda i: flib.rxq4_floor_stream(big.data_ptr(), 2 << 30, sink.data_ptr(),
+                                                                 blocks, 4, nt, sp), 3)
+            sweep[f"nt{nt}_b{blocks}"] = round((2 << 30) / med / 1e3, 1)
+    best = max(sweep, key=sweep.get)
+    floors["stream_read_2GiB"] = {"bytes": 2 << 30, "GBps": sweep[best],
+                                  "pct_of_peak": round(100 * sweep[best] / HBM_PEAK_GBS, 1),
+                                  "kernel": f"persistent grid-stride read, {best}", "sweep_GBps": sweep}
+    med, _ = per_launch(lambda i: big.fill_(i & 7), 3)
+    floors["fill_2GiB_GBps"] = round((2 << 30) / med / 1e3, 1)
     del big, sink
     log(f"floors: {floors}")
 

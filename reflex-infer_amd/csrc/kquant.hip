@@ -599,6 +599,7 @@ hipError_t launch_kq_multi(const GemvRange *ranges, const int *types, int n_rang
 // Q6_K rows (reference dequant_embedding_q6k_kernel, q4_gemm.cu:574-616): a
 // thread writes 8 consecutive outputs of one row with one 16-byte store;
 // w = d*sc*(q - 32) is exact in fp32, so the fp16 result is bit-identical.
+// Nontemporal stores, as the Q4_K gather.
 template <bool kBatched>
 __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ dst,
                                                         const uint8_t *__restrict__ w,
@@ -616,8 +617,8 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ d
     if (kBatched) {
         id = ids[i];
         if (id < 0 || id >= n_vocab) {
-            out[0] = u32x4{0, 0, 0, 0};
-            out[1] = u32x4{0, 0, 0, 0};
+            store16_nt(out, u32x4{0, 0, 0, 0});
+            store16_nt(out + 1, u32x4{0, 0, 0, 0});
             return;
         }
     }
@@ -656,8 +657,8 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ d
             packed[2 * m + e] = (uint32_t)f32_to_f16_bits(v0) | ((uint32_t)f32_to_f16_bits(v1) << 16);
         }
     }
-    out[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
-    out[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+    store16_nt(out, u32x4{packed[0], packed[1], packed[2], packed[3]});
+    store16_nt(out + 1, u32x4{packed[4], packed[5], packed[6], packed[7]});
 }
 
 hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int token_id,

@@ -51,6 +51,13 @@ __device__ __forceinline__ u32x4 load16(const void *p) {
     return *reinterpret_cast<const u32x4 *>(p);
 }
 
+// 16-byte store marked nontemporal, for outputs no later access in the
+// kernel reads (the embedding gathers: 4096 fp16 rows of 2048 in 5.65 us
+// against 6.56 us with ordinary stores).
+__device__ __forceinline__ void store16_nt(void *p, u32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(p));
+}
+
 // The (sc, m) pairs of sub-blocks 2*il and 2*il+1 from the three scale dwords
 // s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].  Returns
 // sc_lo | sc_hi << 8 in *sc and m_lo | m_hi << 8 in *mn.  Same values as

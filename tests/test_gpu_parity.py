@@ -87,6 +87,26 @@ def test_embedding_rows_zipf(K):
     assert np.array_equal(host16(out), orc.embed_rows_f16(Wn, K, ids))
 
 
+def test_embedding_rows_full_table_zipf():
+    """BASELINE configs[4] at full size: the [151936 x 2048] Q4_K table of
+    ggml-quantised N(0, 0.02) weights, 4096 Zipf(1.1) ids over the whole
+    vocabulary (repeats allowed, the last row included), bit-exact against
+    the oracle's dequantisation of the addressed rows."""
+    vocab, K = 151936, 2048
+    g = torch.Generator(device="cuda").manual_seed(46)
+    src = torch.randn((vocab, K), generator=g, device="cuda") * 0.02
+    table = capi.quantize_ggml(src, 12)
+    del src
+    ids = util.zipf_ids(47, 4096, vocab)
+    ids[-1] = vocab - 1
+    out = torch.empty((ids.size, K), dtype=torch.float16, device="cuda")
+    capi.embed_rows_f16(out, table, vocab, dev(ids), K)
+    got = host16(out)
+    ref = orc.embed_rows_f16(table.cpu().numpy(), K, ids)
+    assert np.array_equal(got, ref)
+    assert np.unique(ids).size > 1000  # the Zipf draw spreads over the table
+
+
 def test_embedding_special_values():
     """Subnormal, negative and zero scales dequantise bit-exactly too."""
     from tests.test_oracle import random_blocks
