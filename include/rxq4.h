@@ -20,14 +20,21 @@
  *   - fp16/bf16 buffers are raw 16-bit patterns; x must be 16-byte aligned.
  *   - K must be a positive multiple of 256 and at most RXQ4_MAX_K.
  *   - `stream` is a hipStream_t (NULL = null stream).  Calls only enqueue
- *     work; no entry point synchronises the device or the stream.  The one
- *     allocation is the fp32 workspace of the split launches (split-K GEMM
- *     with few output tiles, small-batch products on long rows, decode
- *     attention over long sequences): 48 MiB per (device, stream), made by
- *     the first such launch on that stream, never resized or freed, so a
- *     HIP graph captured on a stream stays valid whatever runs later, and
- *     launches on different streams never share it.  That first allocation
- *     is also legal while the stream is being captured.
+ *     work; no entry point but rxq4_release_workspace synchronises the
+ *     device or the stream.  The one allocation is the fp32 workspace of the
+ *     split launches (split-K GEMM with few output tiles, small-batch
+ *     products on long rows, decode attention over long sequences): 48 MiB
+ *     per (device, stream), made by the first such launch on that stream,
+ *     never resized, and kept until rxq4_release_workspace(stream) frees it,
+ *     so a HIP graph captured on a stream stays valid whatever runs later,
+ *     and launches on different streams never share it.  hipStreamPerThread
+ *     names a different stream in every thread, so its workspace is kept per
+ *     (device, thread).  That first allocation is also legal while the
+ *     stream is being captured.
+ *   - x must be 16-byte aligned (the one alignment rule the reference does
+ *     not have).  Weight blocks need the alignment of their format: Q4_K
+ *     and Q5_K 16 bytes, Q6_K 2 bytes (its 210-byte blocks; a row slice of a
+ *     Q6_K tensor is accepted wherever it starts).
  *   - The return value is a reflex::infer::Status value (RXQ4_STATUS_*).
  *     On an error nothing is launched; rxq4_last_error() says why.
  */
@@ -118,9 +125,10 @@ int rxq4_gemm(void *y, int y_dtype, const void *w, int ggml_type, const void *x,
  * until the process ends) instead of the stream's workspace, so no call ever allocates device
  * memory (no hipMalloc/hipFree/allocating library call).  No counterpart in
  * the reference; it is for callers that cannot allocate: code under HIP graph
- * capture, serving loops, harnesses that forbid allocation.  The split counts
- * are sized so the partials fit the array; a plan needing more is refused
- * (InvalidArgument, nothing launched).  The array keeps the last call's
+ * capture, serving loops, harnesses that forbid allocation.  No shape is
+ * refused for the array's size: the launchers shrink their split counts so
+ * that the partials fit it (the same counts as rxq4_gemm, whose workspace has
+ * the same size, so the results are identical).  The array keeps the last call's
  * contents and every call on a device shares it: calls that overlap on one
  * device (two streams, or two threads) race and must be serialised by the
  * caller. */
@@ -190,6 +198,15 @@ long long rxq4_host_gemv_calls(void);
  * current device now, so that no later call on that stream allocates
  * (optional; no reference counterpart, the reference splits nothing). */
 int rxq4_reserve_workspace(void *stream);
+
+/* NEW.  Synchronises `stream` and frees its workspace on the current device
+ * (for hipStreamPerThread: the calling thread's); Success also when it has
+ * none.  For callers that create streams per request and would otherwise
+ * keep 48 MiB per stream.  A graph captured with split launches on that
+ * stream must not be replayed afterwards (its partials would point at
+ * freed memory); the next split launch on the stream allocates again.  No
+ * reference counterpart. */
+int rxq4_release_workspace(void *stream);
 
 /* Pointer resolution of the reference (q4_gemm.cu:111-135): returns
  * w_device if non-NULL, else w if the HIP runtime reports it as device or

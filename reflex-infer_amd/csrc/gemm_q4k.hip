@@ -1172,30 +1172,16 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
         }
         return hipGetLastError();
     }
-    int splits = 1;
-    if (t2 * kWaves < 1024 && nb >= 16) splits = std::max(1, std::min(cus / t2, nb / 8));
-    // the fp32 partials (splits x n_tok x M) must fit the scratch
-    splits = (int)std::min<size_t>(
-        splits, std::max<size_t>(1, sc.capacity() / ((size_t)n_tok * M * sizeof(float))));
-    if (t2 * kWaves >= 1024 || splits > 1) {
-        const int sbps = (nb + splits - 1) / splits;
-        splits = (nb + sbps - 1) / sbps;
-        float *ws = nullptr;
-        if (splits > 1) {
-            hipError_t e = sc.get(st, (size_t)splits * n_tok * M * sizeof(float), &ws);
-            if (e != hipSuccess) return e;
-        }
-        const dim3 grid(t2, splits);
+    // Short rows (nb < 16): the register kernel, never split over K (every
+    // row is at most 15 super-blocks, dealt to the waves of one workgroup).
+    if (t2 * kWaves >= 1024) {
+        const dim3 grid(t2, 1);
         if (wide)
             gemv_tokens_kernel<XT, YT, 2, kWaves, true>
-                <<<grid, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, ws, sbps);
+                <<<grid, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
         else
             gemv_tokens_kernel<XT, YT, 2, kWaves, false>
-                <<<grid, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, ws, sbps);
-        if (splits > 1) {
-            const int64_t n = (int64_t)n_tok * M;
-            tokens_reduce_kernel<YT><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(y, ws, n, splits);
-        }
+                <<<grid, kWaves * 64, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
     } else {
         const int t1 = (M + 15) / 16;
         if (wide)

@@ -8,11 +8,15 @@
 namespace rxq4 {
 
 // The fp32 workspace of the split launches (split-K partials, attention
-// chunks): kWorkspaceBytes per (device, stream), allocated by the first split
-// launch on that stream, never resized or freed.  Launchers choose split
-// counts whose partials fit in it.
+// chunks): kWorkspaceBytes per (device, stream) (per (device, thread) for
+// hipStreamPerThread), allocated by the first split launch on that stream,
+// never resized, freed only by release_stream_workspace.  Launchers choose
+// split counts whose partials fit in it.
 constexpr size_t kWorkspaceBytes = size_t(48) << 20;
 hipError_t stream_workspace(hipStream_t stream, float **ws);
+// Synchronises `stream` and frees its workspace (*released = 1), or does
+// nothing if it has none (*released = 0).
+hipError_t release_stream_workspace(hipStream_t stream, int *released);
 
 // Where a split launch keeps its fp32 partials: `ptr` (device memory of
 // `bytes` bytes, supplied by the caller) or, when ptr is null, the stream's

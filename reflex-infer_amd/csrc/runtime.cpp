@@ -4,16 +4,19 @@
 // Workspace (split-K GEMM partials, small-batch K-split partials,
 // decode-attention chunk partials):
 // One buffer of kWorkspaceBytes per (device, stream), allocated the first
-// time a split launch is enqueued on that stream and never resized or freed
-// until the process ends.  Hence:
+// time a split launch is enqueued on that stream and kept until
+// rxq4_release_workspace frees it or the process ends.  Hence:
 //   * a HIP graph captured on a stream keeps a valid workspace pointer for
-//     the life of the process, whatever is launched later, on any stream;
+//     as long as the buffer is not released, whatever is launched later;
 //   * split launches on different streams never share memory; launches on
-//     one stream are ordered by the stream itself;
-//   * no entry point synchronises: the only runtime call is the one
-//     hipMalloc per (device, stream), made with the calling thread's capture
-//     mode set to relaxed so that it is also legal while the stream is
-//     being captured (the allocation is not part of the graph).
+//     one stream are ordered by the stream itself.  hipStreamPerThread is one
+//     handle value for many streams (each thread's own default stream), so
+//     its buffers are kept per (device, thread); the legacy null stream is
+//     one stream for all threads and serialises them, so it has one buffer;
+//   * no launch synchronises: the only runtime call is the one hipMalloc per
+//     (device, stream), made with the calling thread's capture mode set to
+//     relaxed so that it is also legal while the stream is being captured
+//     (the allocation is not part of the graph).
 // Every split launcher sizes its split count so that its partials fit.
 #include <hip/hip_runtime_api.h>
 
@@ -21,6 +24,8 @@
 #include <cstdlib>
 #include <map>
 #include <mutex>
+#include <thread>
+#include <tuple>
 #include <utility>
 
 #include "launch.h"
@@ -29,16 +34,28 @@ namespace rxq4 {
 
 namespace {
 std::mutex g_mutex;
-std::map<std::pair<int, uintptr_t>, void *> *g_buffers = nullptr;  // never destroyed
+// (device, stream handle, thread id or 0) -> buffer
+using WsKey = std::tuple<int, uintptr_t, size_t>;
+std::map<WsKey, void *> *g_buffers = nullptr;  // never destroyed
+
+hipError_t workspace_key(hipStream_t st, WsKey *key) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const size_t tid = st == hipStreamPerThread
+                           ? std::hash<std::thread::id>()(std::this_thread::get_id()) | 1u
+                           : 0u;
+    *key = WsKey(dev, reinterpret_cast<uintptr_t>(st), tid);
+    return hipSuccess;
+}
 }  // namespace
 
 hipError_t stream_workspace(hipStream_t st, float **ws) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    WsKey key;
+    hipError_t e = workspace_key(st, &key);
     if (e != hipSuccess) return e;
-    const auto key = std::make_pair(dev, reinterpret_cast<uintptr_t>(st));
     std::lock_guard<std::mutex> lock(g_mutex);
-    if (!g_buffers) g_buffers = new std::map<std::pair<int, uintptr_t>, void *>();
+    if (!g_buffers) g_buffers = new std::map<WsKey, void *>();
     auto it = g_buffers->find(key);
     if (it == g_buffers->end()) {
         hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
@@ -51,6 +68,27 @@ hipError_t stream_workspace(hipStream_t st, float **ws) {
         it = g_buffers->emplace(key, p).first;
     }
     *ws = static_cast<float *>(it->second);
+    return hipSuccess;
+}
+
+hipError_t release_stream_workspace(hipStream_t st, int *released) {
+    *released = 0;
+    WsKey key;
+    hipError_t e = workspace_key(st, &key);
+    if (e != hipSuccess) return e;
+    void *p = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if (!g_buffers) return hipSuccess;
+        auto it = g_buffers->find(key);
+        if (it == g_buffers->end()) return hipSuccess;
+        p = it->second;
+        g_buffers->erase(it);
+    }
+    // the stream's queued work may still use the buffer
+    if ((e = hipStreamSynchronize(st)) != hipSuccess) return e;
+    if ((e = hipFree(p)) != hipSuccess) return e;
+    *released = 1;
     return hipSuccess;
 }
 

@@ -57,6 +57,15 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 bool kquant_type(int t) { return t == RXQ4_GGML_TYPE_Q5_K || t == RXQ4_GGML_TYPE_Q6_K; }
 
+// Weight alignment each format's kernels need: Q4_K / Q5_K blocks are read
+// with 16-byte loads; Q6_K's 210-byte blocks are only 2-byte aligned in a
+// tensor, and its kernels read every field with dword-aligned loads from the
+// dword at or below the row and realign (so any row slice is accepted).
+bool weights_aligned(const void *w, int ggml_type) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w);
+    return ggml_type == RXQ4_GGML_TYPE_Q6_K ? (a & 1u) == 0 : (a & 15u) == 0;
+}
+
 // Checks shared by every weight-streaming entry point.
 int check_common(const char *fn, const void *w, int ggml_type, int K) {
     if (ggml_type != RXQ4_GGML_TYPE_Q4_K && !kquant_type(ggml_type))
@@ -67,8 +76,10 @@ int check_common(const char *fn, const void *w, int ggml_type, int K) {
         return set_error(RXQ4_STATUS_INVALID_ARGUMENT,
                     "%s: K=%d must be a positive multiple of 256 and <= %d", fn, K, RXQ4_MAX_K);
     if (!w) return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null weight pointer", fn);
-    if (!aligned16(w))
-        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights must be 16-byte aligned", fn);
+    if (!weights_aligned(w, ggml_type))
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT,
+                         "%s: weights must be %d-byte aligned for ggml_type %d", fn,
+                         ggml_type == RXQ4_GGML_TYPE_Q6_K ? 2 : 16, ggml_type);
     return RXQ4_STATUS_SUCCESS;
 }
 
@@ -261,8 +272,16 @@ hipError_t scratch_address(float **p) {
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     float *a = g_scratch_addr[dev].load(std::memory_order_acquire);
     if (!a) {
+        // The first call may come while the caller's stream is being captured
+        // (the entry point is for graph capture): the lookup is not part of
+        // any graph, so it runs with this thread's capture mode relaxed.
         void *q = nullptr;
-        if ((e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        if ((e = hipThreadExchangeStreamCaptureMode(&mode)) != hipSuccess) return e;
+        e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+        hipStreamCaptureMode back = mode;
+        (void)hipThreadExchangeStreamCaptureMode(&back);
+        if (e != hipSuccess) return e;
         a = static_cast<float *>(q);
         g_scratch_addr[dev].store(a, std::memory_order_release);
     }
@@ -300,8 +319,9 @@ int rxq4_embed_row_f16(void *dst, const void *w, int ggml_type, int token_id, in
     // Q4_K and Q6_K, as the reference (q4_gemm.cu:2089-2106).
     if (ggml_type != RXQ4_GGML_TYPE_Q4_K && ggml_type != RXQ4_GGML_TYPE_Q6_K)
         return set_error(RXQ4_STATUS_UNSUPPORTED_QUANT_FORMAT, "%s: ggml_type %d", fn, ggml_type);
-    if (!aligned16(w) || !dst || !aligned16(dst))
-        return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: weights/dst must be 16-byte aligned", fn);
+    if (!weights_aligned(w, ggml_type) || !dst || !aligned16(dst))
+        return set_error(RXQ4_STATUS_INVALID_ARGUMENT,
+                         "%s: misaligned weights (Q4_K 16 bytes, Q6_K 2) or dst (16 bytes)", fn);
     if (!rxq4::device_info().arch_ok)
         return set_error(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
     const auto launch = ggml_type == RXQ4_GGML_TYPE_Q6_K ? rxq4::launch_kq_embed : rxq4::launch_embed;
@@ -322,7 +342,7 @@ int rxq4_embed_rows_f16(void *dst, const void *w, int ggml_type, int64_t n_vocab
         return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: n_ids=%d n_vocab=%lld", fn, n_ids,
                     (long long)n_vocab);
     if (n_ids == 0) return ok();
-    if (!ids || !dst || !aligned16(w) || !aligned16(dst))
+    if (!ids || !dst || !weights_aligned(w, ggml_type) || !aligned16(dst))
         return set_error(RXQ4_STATUS_INVALID_ARGUMENT, "%s: null/misaligned pointer", fn);
     if (!rxq4::device_info().arch_ok)
         return set_error(RXQ4_STATUS_UNSUPPORTED_DEVICE, "%s: current device is not gfx950", fn);
@@ -448,6 +468,12 @@ int rxq4_reserve_workspace(void *stream) {
     float *ws = nullptr;
     return from_hip(rxq4::stream_workspace(static_cast<hipStream_t>(stream), &ws),
                     "rxq4_reserve_workspace");
+}
+
+int rxq4_release_workspace(void *stream) {
+    int released = 0;
+    return from_hip(rxq4::release_stream_workspace(static_cast<hipStream_t>(stream), &released),
+                    "rxq4_release_workspace");
 }
 
 const char *rxq4_version(void) { return "rxq4 0.1.0 gfx950"; }

@@ -48,6 +48,7 @@ SIGNATURES = {
                                c_int]),
     "rxq4_host_gemv_calls": (ctypes.c_longlong, []),
     "rxq4_reserve_workspace": (c_int, [c_void_p]),
+    "rxq4_release_workspace": (c_int, [c_void_p]),
     "rxq4_resolve_weights": (c_void_p, [c_void_p, c_void_p]),
     "rxq4_version": (ctypes.c_char_p, []),
     "rxq4_last_error": (ctypes.c_char_p, []),
@@ -219,3 +220,7 @@ def host_gemv_calls() -> int:
 
 def reserve_workspace(stream=None):
     return _check(lib().rxq4_reserve_workspace(_stream(stream)), "rxq4_reserve_workspace")
+
+
+def release_workspace(stream=None):
+    return _check(lib().rxq4_release_workspace(_stream(stream)), "rxq4_release_workspace")

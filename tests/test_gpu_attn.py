@@ -39,14 +39,18 @@ def check(got_bits, ref64, ref32):
 
 
 # (n_heads, n_kv, head_dim, seq_len): GQA 4 (Qwen3-4B-like), MHA, one KV head
-# for 16 query heads (two head groups per KV head), head_dim 64/80/256,
-# empty / one / tile-boundary / multi-chunk sequences; 7000, 8192 and 16384
-# positions split into 55 and 64 chunks of several tiles each (the combine's
-# maximum of 64).
+# for 16 query heads (the matrix-core kernel's largest group: one workgroup
+# per KV head, all 16 heads in its MFMA columns), groups of 6 and 7 (12/2 and
+# 28/4 heads: zero-padded MFMA columns), a group of 32 (32/1 heads: past the
+# matrix-core kernel's 16, the VALU kernel with four 8-head groups per KV
+# head), head_dim 64/80/256, empty / one / tile-boundary / multi-chunk
+# sequences; 7000, 8192 and 16384 positions split into 55 and 64 chunks of
+# several tiles each (the combine's maximum of 64).
 DECODE = [(32, 8, 128, 0), (32, 8, 128, 1), (32, 8, 128, 256), (32, 8, 128, 257),
           (32, 8, 128, 1500), (32, 8, 128, 4097), (8, 8, 64, 700), (16, 1, 128, 3000),
           (4, 2, 80, 333), (4, 1, 256, 2100), (16, 1, 128, 7000), (32, 8, 128, 8192),
-          (32, 8, 128, 16384)]
+          (32, 8, 128, 16384), (12, 2, 128, 1000), (28, 4, 128, 2500), (32, 1, 128, 1800),
+          (32, 1, 64, 600)]
 
 
 @pytest.mark.parametrize("H,KV,D,S", DECODE)
@@ -68,8 +72,10 @@ def test_decode_fp16(H, KV, D, S):
 
 
 # (n_heads, n_kv, head_dim): the matrix-core decode kernel at head_dim 128
-# (GQA 4) and 64 (GQA 8), and the VALU kernel at head_dim 80 (GQA 2)
-@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (16, 2, 64), (8, 4, 80)])
+# (GQA 4, 6 and 7) and 64 (GQA 8), and the VALU kernel at head_dim 80 (GQA 2)
+# and at head_dim 128 with a group of 32
+@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (16, 2, 64), (8, 4, 80), (12, 2, 128),
+                                    (28, 4, 128), (32, 1, 128)])
 @pytest.mark.parametrize("scales", [True, False])
 @pytest.mark.parametrize("S", [2000, 9000])
 def test_decode_int8(H, KV, D, scales, S):
@@ -133,8 +139,8 @@ def test_decode_api_matches_c_abi():
 # 128 (matrix-core prefill) and 80 (VALU kernel), N not a multiple of the
 # token block, int8 with and without scales.  The last two have more
 # workgroups (8 KV heads x 33-34 blocks of 16 tokens) than the 256 CUs and
-# take the one-group kernel (V^T staged by the threads); the others the
-# two-group kernel (V read back with transposing LDS reads).
+# take the one-group kernel; the others the two-group kernel (both stage V
+# row-major and read it back with transposing LDS reads).
 PREFILL = [(32, 8, 128, 100, 0, False), (16, 4, 128, 300, 37, False), (8, 8, 64, 70, 5, False),
            (16, 2, 64, 33, 200, False), (32, 1, 128, 20, 10, False), (12, 2, 128, 17, 3, False),
            (16, 4, 128, 50, 64, "scales"), (8, 2, 64, 40, 0, "plain"), (4, 2, 80, 9, 4, False),

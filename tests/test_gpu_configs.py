@@ -247,6 +247,70 @@ def test_reserve_workspace():
     capi.reserve_workspace(s)  # idempotent
 
 
+def test_release_workspace_then_split_launch_allocates_again():
+    M, N, K = 2048, 512, 11008  # split-K: 32 MiB of partials in the stream's workspace
+    W = qweights(960, M, K)
+    g = torch.Generator(device="cuda").manual_seed(961)
+    x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+    ref = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+    capi.gemm(ref, W, x, M, N, K)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    capi.release_workspace(s)  # nothing to release: still Success
+    for rep in range(2):
+        y = torch.empty_like(ref)
+        with torch.cuda.stream(s):
+            capi.gemm(y, W, x, M, N, K, stream=s)
+        capi.release_workspace(s)  # synchronises s, then frees its buffer
+        assert torch.equal(y, ref), rep
+
+
+def test_per_thread_stream_workspaces_are_separate():
+    """hipStreamPerThread is one handle for a different stream in every
+    thread: two threads running split-K GEMMs on it at the same time must not
+    share the split partials."""
+    import ctypes
+    import threading
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    PER_THREAD = 2  # hipStreamPerThread
+    M, N, K = 2048, 512, 11008
+    cases = []
+    for i in range(2):
+        W = qweights(970 + i, M, K)
+        g = torch.Generator(device="cuda").manual_seed(975 + i)
+        x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+        ref = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+        capi.gemm(ref, W, x, M, N, K)
+        cases.append((W, x, ref, [torch.empty_like(ref) for _ in range(4)]))
+    torch.cuda.synchronize()
+    errors = []
+    start = threading.Barrier(2)
+
+    def worker(i):
+        try:
+            torch.cuda.set_device(0)
+            W, x, _, outs = cases[i]
+            start.wait()
+            for y in outs:
+                capi.gemm(y, W, x, M, N, K, stream=PER_THREAD)
+            assert hip.hipStreamSynchronize(PER_THREAD) == 0
+            capi.release_workspace(PER_THREAD)
+        except Exception as ex:  # reported by the main thread
+            errors.append(repr(ex))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i, (_, _, ref, outs) in enumerate(cases):
+        for j, y in enumerate(outs):
+            assert torch.equal(y, ref), (i, j)
+
+
 # ------------------------------------------------------------- host path
 @pytest.mark.host_path
 @pytest.mark.parametrize("t", [12, 13, 14])

@@ -245,3 +245,50 @@ def test_gemm_random_shapes_all_paths():
         wkind = None if (t == 12 and xt == "f16" and util.gemv_path(N, M, K)) else xt
         ref = orc.kq_gemm_f64(Wn, K, t, xv, wkind)
         assert util.rel_err(y.cpu().numpy(), ref) <= util.TOL, f"case {case}"
+
+
+def test_q6k_row_slice_at_its_natural_2_byte_alignment():
+    """A Q6_K [N x 11008] tensor has 9030-byte rows, so a slice that starts at
+    an odd row sits 2 bytes past a dword (6 past a 16-byte boundary).  The C
+    ABI takes it wherever the slice starts, as the reference does
+    (q4_gemm.cu:2023-2076 check no alignment): GEMV, small batch, GEMM, the
+    mixed triple and the gather on the slice match the oracle on the same rows."""
+    K, N_rows, r0, M = 11008, 129, 1, 100
+    rb = (K // 256) * 210
+    Wn = kb.random_blocks(14, util.rng(790), N_rows, K).reshape(N_rows, rb)
+    W = dev(Wn)
+    Ws = W[r0:r0 + M]
+    assert Ws.data_ptr() % 4 == 2 and Ws.data_ptr() % 16 != 0
+    Wsn = np.ascontiguousarray(Wn[r0:r0 + M])
+    x16 = util.x_f16(791, K)
+    x = dev(x16)
+    ref = orc.kq_gemv_f32(Wsn, K, 14, x16)
+    y32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    capi.gemv_f32(y32, Ws, x, M, K, ggml_type=14)
+    assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL
+    y16 = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_f16(y16, Ws, x, M, K, ggml_type=14)
+    assert util.rounded_ok(host16(y16), ref).all()
+    # the mixed triple with the Q6_K range as the slice
+    Wq = util.weights(792, 64, K)
+    ys = [torch.empty(64, dtype=torch.float16, device="cuda"),
+          torch.empty(M, dtype=torch.float16, device="cuda")]
+    capi.gemv_multi_f16([(ys[0], dev(Wq), 64, 12), (ys[1], Ws, M, 14)], x, K)
+    assert util.rounded_ok(host16(ys[0]), orc.kq_gemv_f32(Wq, K, 12, x16)).all()
+    assert util.rounded_ok(host16(ys[1]), ref).all()
+    # small batch (4 tokens) and the GEMM (40 tokens), fp16 in and out
+    for n in (4, 40):
+        xn16 = util.x_f16(793 + n, (n, K))
+        refn = orc.kq_gemm_f64(Wsn, K, 14, f16(xn16), "f16")
+        yn = torch.empty((n, M), dtype=torch.float16, device="cuda")
+        capi.gemm_f16(yn, Ws, dev(xn16), M, n, K, ggml_type=14)
+        assert util.rounded_ok(host16(yn), refn).all(), n
+    # gather from the sliced table
+    ids = np.array([0, 5, M - 1, 5, M, -2], np.int32)
+    out = torch.empty((ids.size, K), dtype=torch.float16, device="cuda")
+    capi.embed_rows_f16(out, Ws, M, dev(ids), K, ggml_type=14)
+    assert np.array_equal(host16(out), orc.kq_embed_rows_f16(Wsn, K, 14, ids))
+    # a Q4_K slice still needs 16 bytes: refused, nothing launched
+    Wq4 = dev(util.weights(794, 8, K))
+    with pytest.raises(rxq4.RxQ4Error):
+        capi.gemv_f16(torch.empty(4, dtype=torch.float16, device="cuda"), Wq4.view(-1)[2:], x, 4, K)

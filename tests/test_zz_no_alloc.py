@@ -93,3 +93,49 @@ def test_gemm_noalloc_replays_in_a_graph():
         capi.gemm_noalloc(y2, W, x, M, N, K)
         torch.cuda.synchronize()
         assert torch.equal(y2, ref), rep
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys
+sys.path[:0] = sys.argv[1:3]
+import torch
+import rxq4
+from rxq4 import capi
+rxq4.load()
+M, N, K = 2048, 512, 11008
+g = torch.Generator(device="cuda").manual_seed(940)
+W = capi.quantize(torch.randn((M, K), generator=g, device="cuda") * 0.02)
+x = torch.randn((N, K), generator=g, device="cuda").to(torch.bfloat16)
+ref = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+capi.gemm(ref, W, x, M, N, K)
+y = torch.empty_like(ref)
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+# the process's first rxq4_gemm_noalloc call: made while s is captured
+# (torch's global capture mode)
+with torch.cuda.graph(graph, stream=s):
+    capi.gemm_noalloc(y, W, x, M, N, K, stream=s)
+for rep in range(3):
+    with torch.cuda.stream(s):
+        y.fill_(0)
+        graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref), rep
+print("first-call-in-capture ok", flush=True)
+"""
+
+
+def test_gemm_noalloc_first_call_inside_a_capture():
+    """A fresh process whose first rxq4_gemm_noalloc call happens inside a
+    torch graph capture (the lookup of the array's device address runs then):
+    the graph replays bit for bit what rxq4_gemm computes."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    p = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, root,
+                        os.path.join(root, "reflex-infer_amd")],
+                       capture_output=True, text=True, timeout=300)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-4000:]
+    assert "first-call-in-capture ok" in p.stdout
