@@ -1,78 +1,22 @@
 // floors.hip -- measurement kernels for bench.py (not part of the drop-in
-// library): what a launch and a pure stream of the same bytes cost on the
-// box, the floors against which the GEMV kernels are judged.
+// library): what a launch, a sustained read and a sustained write cost on
+// the box, the floors against which the GEMV and gather kernels are judged.
 //   rxq4_floor_empty(stream)                       an empty kernel (one wave)
-//   rxq4_floor_read(src, bytes, sink, blocks, stream)    reads `bytes` (a
-//       multiple of 16) once with `blocks` workgroups of 256 threads: thread
-//       t issues its u = ceil(bytes / 16 / threads) 16-byte loads (at t,
-//       t + threads, ..., coalesced per load; u <= 16) before any use; one
-//       dword per workgroup goes to `sink` so the loads stay live.  bench.py
-//       takes the fastest of a few grid sizes.
-//   rxq4_floor_read_runs(src, bytes, sink, run_kb, stream)    reads `bytes`
-//       (a multiple of 1024) as contiguous runs of `run_kb` KB (1..32), one
-//       run per wave, 4 waves per workgroup: lane l of the wave loads 16
-//       bytes at run + 1024*j + 16*l for every j, all before any use (the
-//       access pattern of a GEMV wave that streams whole rows).
 //   rxq4_floor_stream(src, bytes, sink, blocks, unroll, nt, stream)    a
 //       persistent grid-stride read: `blocks` workgroups of 256 threads
 //       loop over the buffer, each lane keeping two batches of `unroll`
 //       (4, 8 or 16) 16-byte loads in flight (load j of a batch at
 //       i + j * threads, coalesced across the grid); nt = 1 marks the loads
 //       nontemporal.  The read ceiling the GEMVs are compared with.
+//   rxq4_floor_write(dst, bytes, blocks, nt, stream)    a grid-stride
+//       16-byte store of zeros over `bytes` (nt = 1: nontemporal stores),
+//       the write rate the embedding gathers are compared with.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __global__ void floor_empty_kernel() {}
-
-template <int U>
-__global__ __launch_bounds__(256) void floor_read_kernel(const u32x4 *__restrict__ src,
-                                                         int64_t n16, uint32_t *sink) {
-    const int64_t threads = (int64_t)gridDim.x * 256;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    u32x4 v[U];
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-        const int64_t i = t + j * threads;
-        v[j] = i < n16 ? src[i] : u32x4{0, 0, 0, 0};
-    }
-    uint32_t acc = 0;
-#pragma unroll
-    for (int j = 0; j < U; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
-    __shared__ uint32_t red[256];
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t s = 0;
-        for (int i = 0; i < 256; ++i) s ^= red[i];
-        sink[blockIdx.x] = s;
-    }
-}
-
-template <int R>
-__global__ __launch_bounds__(256) void floor_runs_kernel(const uint8_t *__restrict__ src,
-                                                         int64_t n_runs, uint32_t *sink) {
-    const int lane = threadIdx.x & 63;
-    const int64_t run = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    uint32_t acc = 0;
-    if (run < n_runs) {
-        const uint8_t *p = src + run * (R * 1024) + 16 * lane;
-        u32x4 v[R];
-#pragma unroll
-        for (int j = 0; j < R; ++j) v[j] = *reinterpret_cast<const u32x4 *>(p + 1024 * j);
-#pragma unroll
-        for (int j = 0; j < R; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
-    }
-    __shared__ uint32_t red[256];
-    red[threadIdx.x] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t s = 0;
-        for (int i = 0; i < 256; ++i) s ^= red[i];
-        sink[blockIdx.x] = s;
-    }
-}
 
 // Persistent grid-stride read, two batches of U 16-byte loads in flight per
 // lane.  Loads are unconditional (indices past the end clamp to the last
@@ -130,44 +74,6 @@ extern "C" {
 
 int rxq4_floor_empty(void *stream) {
     floor_empty_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>();
-    return hipGetLastError() == hipSuccess ? 0 : 1;
-}
-
-// sink: at least `blocks` dwords
-int rxq4_floor_read(const void *src, int64_t bytes, uint32_t *sink, int blocks, void *stream) {
-    if (bytes <= 0 || bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(src) & 15) != 0) return 4;
-    if (blocks <= 0) return 4;
-    const int64_t n16 = bytes / 16;
-    const int64_t u = (n16 + (int64_t)blocks * 256 - 1) / ((int64_t)blocks * 256);
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    const u32x4 *s = static_cast<const u32x4 *>(src);
-    if (u <= 1) floor_read_kernel<1><<<blocks, 256, 0, st>>>(s, n16, sink);
-    else if (u <= 2) floor_read_kernel<2><<<blocks, 256, 0, st>>>(s, n16, sink);
-    else if (u <= 4) floor_read_kernel<4><<<blocks, 256, 0, st>>>(s, n16, sink);
-    else if (u <= 8) floor_read_kernel<8><<<blocks, 256, 0, st>>>(s, n16, sink);
-    else if (u <= 16) floor_read_kernel<16><<<blocks, 256, 0, st>>>(s, n16, sink);
-    else return 4;
-    return hipGetLastError() == hipSuccess ? 0 : 1;
-}
-
-// sink: at least ceil(bytes / (run_kb KB) / 4) dwords
-int rxq4_floor_read_runs(const void *src, int64_t bytes, uint32_t *sink, int run_kb, void *stream) {
-    if (bytes <= 0 || (reinterpret_cast<uintptr_t>(src) & 15) != 0) return 4;
-    if (run_kb < 1 || run_kb > 32 || bytes % ((int64_t)run_kb * 1024) != 0) return 4;
-    const int64_t n_runs = bytes / ((int64_t)run_kb * 1024);
-    const int64_t blocks = (n_runs + 3) / 4;
-    if (blocks > 0x7FFFFFFF) return 4;
-    const hipStream_t st = static_cast<hipStream_t>(stream);
-    const uint8_t *s = static_cast<const uint8_t *>(src);
-    switch (run_kb) {
-    case 1: floor_runs_kernel<1><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
-    case 2: floor_runs_kernel<2><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
-    case 4: floor_runs_kernel<4><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
-    case 8: floor_runs_kernel<8><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
-    case 16: floor_runs_kernel<16><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
-    case 32: floor_runs_kernel<32><<<(unsigned)blocks, 256, 0, st>>>(s, n_runs, sink); break;
-    default: return 4;
-    }
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 

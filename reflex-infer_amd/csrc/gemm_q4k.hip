@@ -75,7 +75,7 @@ namespace rxq4 {
 // adds the splits in split order and writes the output, so results do not
 // depend on scheduling.  The kernel boundary between the two launches is the
 // only synchronisation (no atomics, fences or spinning).
-constexpr int kRowsPerWg = 256;
+constexpr int kRowsPerWg = 256;  // rows of the eight-wave workgroup
 constexpr int kRing = 4;  // LDS stage buffers; stage s uses buffer s % 4
 
 struct GemmParams {
@@ -91,7 +91,9 @@ struct GemmParams {
 };
 
 constexpr int kW8Rows = 32;                       // weight rows per wave
-constexpr int kOutPitch = kRowsPerWg * 2 + 16;    // staged output: bytes per token
+// staged output of an NW-wave workgroup (32 * NW rows): bytes per token
+template <int NW>
+constexpr int out_pitch() { return 64 * NW + 16; }
 
 // ---------------------------------------------------------------------------
 // Weight formats of the GEMM.  A stage is 64 weights of every row; lane
@@ -319,21 +321,25 @@ struct GemmFmt<14> {
 };
 
 // LDS of one workgroup: the x ring, reused for the staged output tile.
-template <int TM>
+template <int TM, int NW = 8>
 constexpr int gemm_lds_bytes() {
-    return TM * kOutPitch > kRing * TM * 128 ? TM * kOutPitch : kRing * TM * 128;
+    return TM * out_pitch<NW>() > kRing * TM * 128 ? TM * out_pitch<NW>() : kRing * TM * 128;
 }
 
-// One output tile: rows [256 * row_tile, +256) x tokens [TM * tok_tile, +TM)
+// One output tile of an NW-wave workgroup (NW = 8: two waves per SIMD; 4:
+// one): rows [32 * NW * row_tile, +32 * NW) x tokens [TM * tok_tile, +TM)
 // over super-blocks [split * sb_per_split, +sb_per_split).
-template <int T, int XT, int YT, int TM>
+template <int T, int XT, int YT, int TM, int NW = 8>
 __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int split,
                                           int row_tile, int tok_tile) {
     using F = GemmFmt<T>;
     // TM tokens per workgroup tile (128 or 256)
     constexpr int NT = TM / 32;      // 32-token fragments per wave
     constexpr int MPS = 4 * NT;      // MFMAs per stage and wave
-    constexpr int kXLoads = TM / 64; // 1 KB direct-to-LDS copies per wave per stage
+    constexpr int RPW = 32 * NW;     // weight rows per workgroup
+    constexpr int THREADS = 64 * NW;
+    constexpr int kOutPitch = out_pitch<NW>();
+    constexpr int kXLoads = TM / (8 * NW); // 1 KB direct-to-LDS copies per wave per stage
     constexpr int kQLoads = F::kQLoads, kHLoads = F::kHLoads;
     constexpr int kLook = 6;         // B fragments are read kLook MFMAs before use
     constexpr int kBufBytes = TM * 128;                        // one stage of x
@@ -349,7 +355,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int
     const int h = lane >> 5;    // half of the stage's weights of the row
     const int K = p.K;
     const int64_t row_bytes = (int64_t)p.nb * F::kBytes;
-    const int row_base = row_tile * kRowsPerWg + wave * kW8Rows;
+    const int row_base = row_tile * RPW + wave * kW8Rows;
     const int tok_base = tok_tile * TM;
 
     typename F::Loader ld;
@@ -368,9 +374,10 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int
     ld.nsb = nsb;
     ld.h = h;
 
-    // Direct-to-LDS copies of the x tile: 16 chunks of 1 KB (8 tokens) per
-    // stage, chunks wave and wave + 8 (tokens 8*chunk + lane/8); chunk c of
-    // token t at c ^ ((t >> 1) & 7), and (t >> 1) & 7 = 4*(wave & 1) + lane/16.
+    // Direct-to-LDS copies of the x tile: TM / 8 chunks of 1 KB (8 tokens)
+    // per stage, chunks wave + NW * i (tokens 8*chunk + lane/8); chunk c of
+    // token t at c ^ ((t >> 1) & 7), and (t >> 1) & 7 = 4*(wave & 1) + lane/16
+    // (NW is even, so chunk parity is wave parity).
     const int ctok = lane >> 3;
     const int cpos = (lane & 7) ^ ((4 * (wave & 1) + (ctok >> 1)) & 7);
     const __amdgpu_buffer_rsrc_t xrsrc =
@@ -378,7 +385,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int
     int xoff[kXLoads];
 #pragma unroll
     for (int i = 0; i < kXLoads; ++i) {
-        const int tok = min(8 * (wave + 8 * i) + ctok, p.N - 1 - tok_base);
+        const int tok = min(8 * (wave + NW * i) + ctok, p.N - 1 - tok_base);
         xoff[i] = (tok * K + F::chunk_elem(cpos)) * 2;
     }
     // Stage s's copies (clamped to the last stage) into ring buffer s % 4;
@@ -387,7 +394,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int
         const int k0b = (sb0 * 256 + F::stage_elem(min(s, n_stages - 1))) * 2;
 #pragma unroll
         for (int i = 0; i < kXLoads; ++i)
-            buffer_to_lds16(xrsrc, lds + buf * kBufBytes + (wave + 8 * i) * 1024, xoff[i], k0b);
+            buffer_to_lds16(xrsrc, lds + buf * kBufBytes + (wave + NW * i) * 1024, xoff[i], k0b);
     };
 
     // Per-lane byte offset of B fragment (k-step k, token fragment 0) in a
@@ -492,18 +499,18 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int
     if (p.splits > 1) {
         // partial tile: per thread NT x 4 float4 in (tf, j) order
         f32x4 *part = reinterpret_cast<f32x4 *>(p.ws) +
-                      ((int64_t)(tile * p.splits + split) * (4 * NT)) * 512 + tid;
+                      ((int64_t)(tile * p.splits + split) * (4 * NT)) * THREADS + tid;
 #pragma unroll
         for (int tf = 0; tf < NT; ++tf)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                part[(tf * 4 + j) * 512] = f32x4{acc[tf][4 * j], acc[tf][4 * j + 1],
+                part[(tf * 4 + j) * THREADS] = f32x4{acc[tf][4 * j], acc[tf][4 * j + 1],
                                                  acc[tf][4 * j + 2], acc[tf][4 * j + 3]};
         return;
     }
     if (YT != RXQ4_DTYPE_F32 && (p.M & 7) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0) {
-        // Stage the tile as [token][256 rows] (16-bit) in the ring, then
-        // write 16 bytes per lane: 32 lanes cover one token's rows.
+        // Stage the tile as [token][RPW rows] (16-bit) in the ring, then
+        // write 16 bytes per lane: RPW / 8 lanes cover one token's rows.
         lds_barrier();  // every wave is done reading the ring
         uint8_t *ot = lds;
 #pragma unroll
@@ -527,10 +534,11 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int
             }
         wait_lgkmcnt0();
         lds_barrier();
-        const int row0 = row_tile * kRowsPerWg;
+        const int row0 = row_tile * RPW;
+        constexpr int LPT = RPW / 8;  // lanes per token
 #pragma unroll
-        for (int i = 0; i < TM * 32 / 512; ++i) {
-            const int id = tid + 512 * i, t = id >> 5, c = id & 31;
+        for (int i = 0; i < TM * LPT / THREADS; ++i) {
+            const int id = tid + THREADS * i, t = id / LPT, c = id % LPT;
             const int tok = tok_base + t, row = row0 + 8 * c;
             if (tok < p.N && row < p.M)  // M % 8 == 0: all 8 rows are in range
                 *reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(p.y) + (int64_t)tok * p.M + row) =
@@ -555,9 +563,9 @@ __device__ __forceinline__ void gemm_tile(const GemmParams &p, uint8_t *lds, int
         }
 }
 
-template <int T, int XT, int YT, int TM>
-__global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[gemm_lds_bytes<TM>()];
+template <int T, int XT, int YT, int TM, int NW = 8>
+__global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[gemm_lds_bytes<TM, NW>()];
     const int L = blockIdx.x;
     const int V = (L % 8) * p.units_per_xcd + L / 8;  // consecutive units share an XCD
     if (V >= p.total_units) return;
@@ -581,7 +589,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
         row_tile = t / p.tok_tiles;
         tok_tile = t % p.tok_tiles;
     }
-    gemm_tile<T, XT, YT, TM>(p, lds, split, row_tile, tok_tile);
+    gemm_tile<T, XT, YT, TM, NW>(p, lds, split, row_tile, tok_tile);
 }
 
 // Mixed token tiles for GEMMs that fill the CUs between one and two times
@@ -622,9 +630,10 @@ __global__ __launch_bounds__(512) void gemm_mixed_kernel(GemmParams p) {
 
 // Split-K reduction for gemm_kernel: block (tile, e), e = tf*4 + j, sums
 // float4 e of every thread of the tile over the splits in split order.
-template <int YT, int TM>
-__global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
+template <int YT, int TM, int NW = 8>
+__global__ __launch_bounds__(64 * NW) void gemm_reduce_kernel(GemmParams p) {
     constexpr int E = 4 * (TM / 32);  // float4 per thread
+    constexpr int THREADS = 64 * NW;
     const int tid = threadIdx.x;
     // Block b runs on XCD b % 8 and reduces tiles whose first split ran on
     // that XCD in the row-major unit order (units [x * units_per_xcd,
@@ -639,10 +648,10 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
     const int tf = e / 4, j = e % 4;
     const int row_tile = tile / p.tok_tiles, tok_tile = tile % p.tok_tiles;
     const int lane = tid & 63, wave = tid >> 6;
-    const int row = row_tile * kRowsPerWg + wave * kW8Rows + 8 * j + 4 * (lane >> 5);
+    const int row = row_tile * 32 * NW + wave * kW8Rows + 8 * j + 4 * (lane >> 5);
     const int tok = tok_tile * TM + 32 * tf + (lane & 31);
     const f32x4 *src = reinterpret_cast<const f32x4 *>(p.ws) +
-                       ((int64_t)tile * p.splits * E + e) * 512 + tid;
+                       ((int64_t)tile * p.splits * E + e) * THREADS + tid;
     // Up to 8 splits' loads are in flight before the first add (a loop of
     // dependent load-add steps waits out one memory latency per split); the
     // adds stay in split order.
@@ -651,7 +660,7 @@ __global__ __launch_bounds__(512) void gemm_reduce_kernel(GemmParams p) {
         f32x4 v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            if (sp0 + i < p.splits) v[i] = src[(int64_t)(sp0 + i) * E * 512];
+            if (sp0 + i < p.splits) v[i] = src[(int64_t)(sp0 + i) * E * THREADS];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             if (sp0 + i < p.splits)
@@ -962,9 +971,10 @@ __global__ __launch_bounds__(256) void tokens_reduce_kernel(void *__restrict__ y
     store_out<YT>(y, i, s);
 }
 
-template <int T, int XT, int YT, int TM>
+template <int T, int XT, int YT, int TM, int NW = 8>
 static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, int M, int N,
                                 int K, hipStream_t st, const Scratch &sc) {
+    constexpr int RPW = 32 * NW, THREADS = 64 * NW;
     // 32-bit buffer offsets: the x tile, and a wave's 32 rows of Q6_K weights
     const int64_t row_bytes = (int64_t)(K / 256) * GemmFmt<T>::kBytes;
     if ((int64_t)TM * K * 2 > 0x7FFFFFFF || (T == 14 && row_bytes * kW8Rows > 0x7FFFFFFF))
@@ -977,7 +987,7 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     p.N = N;
     p.K = K;
     p.nb = K / 256;
-    p.row_tiles = (M + kRowsPerWg - 1) / kRowsPerWg;
+    p.row_tiles = (M + RPW - 1) / RPW;
     p.tok_tiles = (N + TM - 1) / TM;
     const int tiles = p.row_tiles * p.tok_tiles;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
@@ -988,7 +998,7 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     splits = std::min(splits, std::max(1, p.nb / 2));
     if (tuning().gemm_splits) splits = tuning().gemm_splits;
     // the fp32 partials (one TM x 256 tile per unit) must fit the scratch
-    const size_t unit_bytes = (size_t)TM * kRowsPerWg * sizeof(float);
+    const size_t unit_bytes = (size_t)TM * RPW * sizeof(float);
     splits = (int)std::min<size_t>(splits, std::max<size_t>(1, sc.capacity() / (unit_bytes * tiles)));
     splits = std::max(1, std::min(splits, p.nb));
     p.sb_per_split = (p.nb + splits - 1) / splits;
@@ -1003,11 +1013,11 @@ static hipError_t launch_gemm_t(void *y, const uint8_t *w, const uint16_t *x, in
     const double x_bytes = 2.0 * N * K, w_bytes = (double)M * row_bytes;
     p.tok_major = tuning().gemm_order ? tuning().gemm_order == 2
                                       : x_bytes + p.tok_tiles * w_bytes < 8 * x_bytes + w_bytes;
-    gemm_kernel<T, XT, YT, TM><<<8 * p.units_per_xcd, 512, 0, st>>>(p);
+    gemm_kernel<T, XT, YT, TM, NW><<<8 * p.units_per_xcd, THREADS, 0, st>>>(p);
     if (splits > 1) {  // 4 * TM / 32 float4 per thread; at most units_per_xcd / splits + 1 tiles per XCD
         constexpr int E = 4 * (TM / 32);
-        gemm_reduce_kernel<YT, TM>
-            <<<8 * E * ((p.units_per_xcd + splits - 1) / splits + 1), 512, 0, st>>>(p);
+        gemm_reduce_kernel<YT, TM, NW>
+            <<<8 * E * ((p.units_per_xcd + splits - 1) / splits + 1), THREADS, 0, st>>>(p);
     }
     return hipGetLastError();
 }
@@ -1087,6 +1097,23 @@ static hipError_t launch_gemm_tm(void *y, const uint8_t *w, const uint16_t *x, i
     }
     if (tuning().gemm_mixed > 0 && T != 14) big = tuning().gemm_mixed;
     if constexpr (T != 14) {
+        // Four-wave workgroups (128-row tiles, one wave per SIMD) for shapes
+        // that the eight-wave plan splits 8 ways or more: twice the tiles
+        // halve the split count and the fp32 partials ([2048 x 11008] and
+        // [2048 x 8192] at m = 512: 32 MiB -> 16 MiB, 42.8 -> 40.0 and
+        // 31.5 -> 29.1 us on one box; shapes split 4 ways or less measured
+        // slower with them).
+        int nw = tuning().gemm_nw;
+        if (nw != 4 && nw != 8 && tm == 128 && big <= 0) {
+            const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+            const int64_t tiles8 = (int64_t)((M + kRowsPerWg - 1) / kRowsPerWg) * ((N + 127) / 128);
+            const int64_t splits8 = std::min<int64_t>(cus / std::max<int64_t>(1, tiles8), (K / 256) / 2);
+            nw = splits8 >= 8 ? 4 : 8;
+        }
+        if (nw == 4) {
+            if (tm == 256) return launch_gemm_t<T, XT, YT, 256, 4>(y, w, x, M, N, K, st, sc);
+            return launch_gemm_t<T, XT, YT, 128, 4>(y, w, x, M, N, K, st, sc);
+        }
         if (big > 0) return launch_gemm_mixed<T, XT, YT>(y, w, x, M, N, K, big, st);
         if (tm == 256) return launch_gemm_t<T, XT, YT, 256>(y, w, x, M, N, K, st, sc);
     }

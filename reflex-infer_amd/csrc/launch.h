@@ -134,7 +134,8 @@ hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, 
 //   RXQ4_ATTN_SPLIT (cap on decode chunks), RXQ4_ATTN_MFMA=0 (VALU prefill),
 //   RXQ4_MULTI_TOKEN_GEMV=0 (2..4 tokens on the MFMA small-batch kernel),
 //   RXQ4_GEMM_TM=128|256 (the GEMM's token tile),
-//   RXQ4_GEMM_ORDER=1|2 (the GEMM's unit order: row-major | token-major).
+//   RXQ4_GEMM_ORDER=1|2 (the GEMM's unit order: row-major | token-major),
+//   RXQ4_GEMM_NW=4|8 (the GEMM's waves per workgroup: 128- or 256-row tiles).
 struct Tuning {
     int gemm_splits = 0;
     int gemv_waves_per_cu = 0;
@@ -147,6 +148,7 @@ struct Tuning {
     int gemm_mixed = 0;  // > 0: mixed token tiles with this many whole areas per XCD
     int tokens_waves = 0;
     int tokens_lds_split = 0;
+    int gemm_nw = 0;  // 4 | 8: force the GEMM's four- or eight-wave workgroup
 };
 const Tuning &tuning();
 

@@ -122,6 +122,7 @@ const Tuning &tuning() {
         r.gemm_mixed = env_pos("RXQ4_GEMM_MIXED");
         r.tokens_waves = env_pos("RXQ4_TOKENS_WAVES");
         r.tokens_lds_split = env_pos("RXQ4_TOKENS_LDS_SPLIT");
+        r.gemm_nw = env_pos("RXQ4_GEMM_NW");
         return r;
     }();
     return t;

@@ -415,6 +415,59 @@ def test_jllm_fast_gemv_0_selects_the_host_path():
     assert "fast-gemv-off ok" in r.stdout
 
 
+FOUR_WAVE_GEMM = r"""
+import sys, numpy as np, torch
+sys.path[:0] = [ROOT, ROOT + "/reflex-infer_amd"]
+import rxq4
+from rxq4 import capi
+from oracle import oracle as orc
+from tests import util
+# (M, N, K, x dtype, y dtype): partial last row and token tiles, one
+# super-block per row, a last token tile of one token, split K over long
+# rows, M % 8 != 0 (direct stores), fp32 / bf16 / fp16 outputs
+CASES = [(2048, 512, 11008, "bf16", "bf16"), (300, 100, 11008, "bf16", "f32"),
+         (1000, 200, 2048, "bf16", "bf16"), (264, 130, 512, "f16", "f16"),
+         (520, 129, 256, "bf16", "bf16"), (250, 40, 2048, "bf16", "f32"),
+         (129, 33, 512, "f16", "f32")]
+for M, N, K, xt, yt in CASES:
+    print("four-wave gemm", M, N, K, xt, yt, flush=True)
+    Wn = util.weights(9300 + M + N, M, K)
+    W = torch.from_numpy(Wn).cuda()
+    if xt == "bf16":
+        xb = util.f32_to_bf16_bits(util.gaussian(9301 + N, (N, K)))
+        xv = orc.bits_bf16_to_f32(xb)
+        x = torch.from_numpy(xb.view(np.int16)).cuda().view(torch.bfloat16)
+    else:
+        x16 = util.x_f16(9302 + N, (N, K))
+        xv = x16.view(np.float16).astype(np.float32)
+        x = torch.from_numpy(x16.view(np.int16)).cuda().view(torch.float16)
+    rows = np.sort(util.rng(9303).choice(M, min(M, 96), replace=False))
+    ref = orc.gemm_f64(np.ascontiguousarray(Wn.reshape(M, -1)[rows]), K, xv, xt)
+    ydt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[yt]
+    y = torch.empty((N, M), dtype=ydt, device="cuda")
+    capi.gemm(y, W, x, M, N, K)
+    if yt == "f32":
+        assert util.rel_err(y.cpu().numpy()[:, rows], ref) <= util.TOL, (M, N, K)
+    else:
+        got = y.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows]
+        assert util.rounded_ok(got, ref, yt).all(), (M, N, K)
+print("four-wave ok", flush=True)
+"""
+
+
+@pytest.mark.parametrize("tm", ["128", "256"])
+def test_prefill_gemm_four_wave_workgroups(tm):
+    """The four-wave GEMM workgroup (128-row tiles, one wave per SIMD), forced
+    for every shape with both token tiles: sampled rows against the fp64
+    product of the kernel's operands (the launcher takes it by itself only
+    for shapes split 8 ways, e.g. [2048 x 11008] at m = 512)."""
+    env = dict(os.environ, RXQ4_GEMM_NW="4", RXQ4_GEMM_TM=tm)
+    r = subprocess.run([sys.executable, "-c", FOUR_WAVE_GEMM.replace("ROOT", repr(ROOT))],
+                       env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-1500:] + r.stderr[-3000:]
+    assert "four-wave ok" in r.stdout
+
+
 # --------------------------------------------------- very long rows, m <= 4
 @pytest.mark.parametrize("M,N,K", [(64, 4, 28672), (64, 3, 24320), (64, 2, 65536),
                                    (64, 4, 16384)])
