@@ -204,6 +204,84 @@ def test_decode_chain_three_layers_in_a_graph():
 
 
 # ------------------------------------------------------------- workspace
+def test_decode36_graph_outputs():
+    """BASELINE configs[1] exactly as bench.py issues it: 36 layers of
+    distinct ggml-quantised weights, fixed fp16 activations (x_h for QKV and
+    gate+up, x_a for O, x_f for down, one residual), 144 reflex::infer calls
+    with weights_device set, captured once and replayed as a HIP graph.  Each
+    call writes its own output here (the bench overwrites one buffer per
+    projection), so every layer's four outputs are checked: bit for bit
+    against the eager calls over two replays, and against the oracle on the
+    same operands."""
+    H, F, L = 2048, 11008, 36
+    Ms = (2048, 256, 256)
+    rb = (H // 256) * 144
+    Ws = [{"qkv": qweights(10_000 + 10 * l + 0, sum(Ms), H), "o": qweights(10_000 + 10 * l + 1, H, H),
+           "gu": qweights(10_000 + 10 * l + 2, 2 * F, H), "down": qweights(10_000 + 10 * l + 3, H, F)}
+          for l in range(L)]
+    x_h, x_a, x_f, res = (dev(util.x_f16(4200 + i, n)) for i, n in enumerate((H, H, F, H)))
+    qkv = [torch.empty(sum(Ms), dtype=torch.float16, device="cuda") for _ in range(L)]
+    o = [torch.empty(H, dtype=torch.float16, device="cuda") for _ in range(L)]
+    gu = [torch.empty(2 * F, dtype=torch.float16, device="cuda") for _ in range(L)]
+    dn = [torch.empty(H, dtype=torch.float16, device="cuda") for _ in range(L)]
+    s = torch.cuda.Stream()
+
+    def step():
+        sp = s.cuda_stream
+        for l in range(L):
+            q = Ws[l]["qkv"].data_ptr()
+            assert api.call("gemv_quant_triple", api.GemvQuantTripleArgs(
+                y0=qkv[l].data_ptr(), weights0=q, weights0_device=q, ggml_type0=12, M0=Ms[0],
+                y1=qkv[l].data_ptr() + 2 * Ms[0], weights1=q + Ms[0] * rb,
+                weights1_device=q + Ms[0] * rb, ggml_type1=12, M1=Ms[1],
+                y2=qkv[l].data_ptr() + 2 * (Ms[0] + Ms[1]), weights2=q + (Ms[0] + Ms[1]) * rb,
+                weights2_device=q + (Ms[0] + Ms[1]) * rb, ggml_type2=12, M2=Ms[2],
+                x=x_h.data_ptr(), K=H, stream=sp)) == rxq4.SUCCESS
+            assert api.call("gemv_quant_add", api.GemvQuantAddArgs(
+                y=o[l].data_ptr(), weights=Ws[l]["o"].data_ptr(),
+                weights_device=Ws[l]["o"].data_ptr(), ggml_type=12, x=x_a.data_ptr(),
+                residual=res.data_ptr(), M=H, K=H, stream=sp)) == rxq4.SUCCESS
+            g = Ws[l]["gu"].data_ptr()
+            assert api.call("gemv_quant_pair", api.GemvQuantPairArgs(
+                y0=gu[l].data_ptr(), weights0=g, weights0_device=g, ggml_type0=12, M0=F,
+                y1=gu[l].data_ptr() + 2 * F, weights1=g + F * rb, weights1_device=g + F * rb,
+                ggml_type1=12, M1=F, x=x_h.data_ptr(), K=H, stream=sp)) == rxq4.SUCCESS
+            assert api.call("gemv_quant_add", api.GemvQuantAddArgs(
+                y=dn[l].data_ptr(), weights=Ws[l]["down"].data_ptr(),
+                weights_device=Ws[l]["down"].data_ptr(), ggml_type=12, x=x_f.data_ptr(),
+                residual=res.data_ptr(), M=H, K=F, stream=sp)) == rxq4.SUCCESS
+
+    outs = qkv + o + gu + dn
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in outs]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step()
+    for rep in range(2):
+        for t in outs:
+            t.fill_(0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, eager):
+            assert torch.equal(a, b), rep
+        with torch.cuda.stream(s):
+            step()  # eager work between the replays
+        torch.cuda.synchronize()
+    xh, xa, xf, r16 = (host16(t) for t in (x_h, x_a, x_f, res))
+    for l in range(L):
+        assert util.rounded_ok(host16(qkv[l]), orc.gemv_f32(Ws[l]["qkv"].cpu().numpy(), H, xh)).all(), l
+        for y, W, xv, K in ((o[l], Ws[l]["o"], xa, H), (dn[l], Ws[l]["down"], xf, F)):
+            y32 = orc.gemv_f32(W.cpu().numpy(), K, xv)
+            sp = util.spacing(orc.f32_to_fp16(y32), "f16")
+            assert util.rounded_ok(host16(y), y32.astype(np.float64) + f16(r16), extra=sp / 2).all(), l
+        assert util.rounded_ok(host16(gu[l]), orc.gemv_f32(Ws[l]["gu"].cpu().numpy(), H, xh)).all(), l
+
+
 def test_graph_workspace_survives_later_split_launches():
     """Capture split-KV decode attention (small workspace use) on a fresh
     stream -- its workspace is allocated during the capture -- then run a
