@@ -426,9 +426,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
 
 // ---------------------------------------------------------------------------
 // Prefill on the matrix cores (head_dim 64 or 128).  A workgroup takes one
-// KV head, HB of its query heads and TPB = 4 * (16 / HB) consecutive tokens;
-// wave w of each of two 4-wave groups owns 16 "query rows" (token, head) =
-// (16 / HB tokens) x (HB heads), all sharing the KV head.  Group q takes the
+// KV head, HB of its query heads and two half blocks of TPB / 2 consecutive
+// tokens (TPB = 4 * (16 / HB)), an early one and the mirror late one, so
+// every workgroup has about the same share of the causal triangle; wave w
+// of each of two 4-wave groups owns 16 "query rows" (token, head) =
+// (16 / HB tokens) x (HB heads), all sharing the KV head (waves 0, 1 the
+// early half block, 2, 3 the late one).  Group q takes the
 // KV tiles 2j + q (its own LDS buffers), so two waves share each SIMD and one
 // wave's softmax and staging overlap the other's MFMAs (the query rows alone
 // give one wave per SIMD: 1024 waves at 512 tokens x 32 heads); at the end
@@ -480,17 +483,33 @@ __global__ __launch_bounds__(256 * G, 2 / G) void attn_prefill_mfma(AttnParams p
     float (*ksc)[kAttnTile] = kscg[q];
     float (*vsc)[kAttnTile] = vscg[q];
     const int r = lane & 15, g = lane >> 4;
-    const int n_tb = (n_tok + TPB - 1) / TPB;
-    const int tb = n_tb - 1 - (int)(blockIdx.x % n_tb);  // longest rows first
-    const int hbk = blockIdx.x / n_tb;
+    // Token half blocks of HPB tokens (two waves of a group); workgroup pr
+    // pairs half block pr (waves 0, 1) with half block n_hbs - 1 - pr
+    // (waves 2, 3), so every workgroup sees about the same number of
+    // visible (query row, position) pairs: the causal triangle is balanced
+    // over the CUs instead of one CU taking the last block's every tile.
+    // With an odd count the middle half block pairs with itself and waves
+    // 2, 3 compute nothing.
+    constexpr int HPB = TPB / 2;
+    const int n_hbs = (n_tok + HPB - 1) / HPB;
+    const int n_pair = (n_hbs + 1) / 2;
+    const int pr = (int)(blockIdx.x % n_pair);
+    const int hbk = blockIdx.x / n_pair;
     const int n_hb = p.group / HB;
     const int kvh = hbk / n_hb;
     const int h = kvh * p.group + (hbk % n_hb) * HB + (r % HB);
-    const int t = tb * TPB + w * TPW + r / HB;
-    const bool row_ok = t < n_tok;
-    const int tc = row_ok ? t : n_tok - 1;
+    const int long_hb = n_hbs - 1 - pr;
+    const int my_hb = w < 2 ? pr : long_hb;
+    const bool dup = w >= 2 && long_hb == pr;
+    const int t = my_hb * HPB + (w & 1) * TPW + r / HB;
+    const bool row_ok = t < n_tok && !dup;
+    const int tc = min(t, n_tok - 1);
     const int qpos = start + tc;  // last visible position of this query row
-    const int pos_end = start + min(n_tok, (tb + 1) * TPB);
+    // the wave's rows see positions [0, wave_end) at most (none when dup);
+    // the workgroup stages tiles up to the long half block's pos_end
+    const int wave_end = dup ? 0 : start + min(n_tok, (my_hb + 1) * HPB);
+    const int blk_first = start + my_hb * HPB;  // first query position of the wave's half block
+    const int pos_end = start + min(n_tok, (long_hb + 1) * HPB);
     const int n_tiles = (pos_end + kAttnTile - 1) / kAttnTile;
     constexpr int esz = I8 ? 1 : 2;
     const int64_t row_stride = (int64_t)p.n_kv * HD * esz;
@@ -609,6 +628,9 @@ __global__ __launch_bounds__(256 * G, 2 / G) void attn_prefill_mfma(AttnParams p
     lds_sync();
     auto compute_tile = [&](int it, int b) {
         const int p0 = it * kAttnTile;
+        // a tile past the wave's visible positions changes nothing (all its
+        // probabilities are 0 and the rescale factor 1): skipped (uniform)
+        if (p0 >= wave_end) return;
         // S^T for the 4 sub-tiles of 16 positions; the causal mask only on
         // tiles that reach past the block's first token (uniform: every
         // other tile is visible to all of the workgroup's rows).
@@ -631,7 +653,7 @@ __global__ __launch_bounds__(256 * G, 2 / G) void attn_prefill_mfma(AttnParams p
                 }
             }
         };
-        if (p0 + kAttnTile - 1 <= start + tb * TPB)
+        if (p0 + kAttnTile - 1 <= blk_first)
             scores(false);
         else
             scores(true);
