@@ -829,8 +829,11 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
     int N, int K, float *__restrict__ ws, int sb_per_split) {
     constexpr int D = 2;             // super-blocks in flight per wave
     constexpr int kBuf = D + 1;
-    constexpr int kXc = 8 / W;       // x copy instructions per wave and super-block
-    static_assert(kXc * W == 8, "workgroup shape");
+    // x copy instructions per wave and super-block: the tile is 8 copies of
+    // 1 KB; with W not dividing 8 the copies j >= 8 repeat copy j % 8 (the
+    // same bytes to the same place), so every wave issues kXc copies and the
+    // vmcnt waits below stay exact
+    constexpr int kXc = (8 + W - 1) / W;
     __shared__ __attribute__((aligned(1024))) uint8_t xs[kBuf][16 * 512];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -848,13 +851,13 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
 #pragma unroll
     for (int t = 0; t < RT; ++t) wr[t] = w + min(row0 + 16 * t + li, M - 1) * row_bytes;
 
-    // x copies: instruction u of wave w covers tokens 2j, 2j + 1 (j = w + W*u);
-    // lane i: token 2j + i/32 (clamped to N - 1), LDS chunk i % 32.
+    // x copies: instruction u of wave w covers tokens 2j, 2j + 1 (j = (w +
+    // W*u) % 8); lane i: token 2j + i/32 (clamped to N - 1), LDS chunk i % 32.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, N * K * 2);
     int xoff[kXc];
 #pragma unroll
     for (int u = 0; u < kXc; ++u) {
-        const int t = 2 * (wave + W * u) + (lane >> 5), p = lane & 31;
+        const int t = 2 * ((wave + W * u) & 7) + (lane >> 5), p = lane & 31;
         xoff[u] = (min(t, N - 1) * K + 8 * (p ^ (t & 15))) * 2;
     }
     // Super-blocks past the end are still loaded, from one fixed line (the
@@ -868,7 +871,7 @@ __global__ __launch_bounds__(W * 64) void gemv_tokens_lds_kernel(
         uint8_t *dst = xs[i % kBuf];
 #pragma unroll
         for (int u = 0; u < kXc; ++u)
-            buffer_to_lds16(xr, dst + (wave + W * u) * 1024, live ? xoff[u] : 16 * (lane & 31),
+            buffer_to_lds16(xr, dst + ((wave + W * u) & 7) * 1024, live ? xoff[u] : 16 * (lane & 31),
                             live ? (sb_lo + i) * 512 : 0);
     };
     struct Sb {
@@ -1163,15 +1166,27 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
     const bool wide = n_tok <= 8;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
     if ((M + 63) / 64 >= cus) {
-        // 64-row workgroups of 4 waves; between one and two of them per CU,
-        // 128-row workgroups of 8 waves (at most one per CU) instead: [22016 x
-        // 2048] m = 16 13.5 -> 11.8 us (344 workgroups put two on 88 CUs).
+        // Workgroups of W = 4, 6 or 8 waves (16 rows each), one per CU when
+        // they fit: W minimises the rows of the busiest CU, 16 W times the
+        // rounds of workgroups (ties to the larger W).  [22016 x 2048]: 230
+        // workgroups of 96 rows (4 waves: 344 put two on 88 CUs, 8 waves:
+        // 172 leave 84 CUs idle; m = 16 13.5 / 11.8 us).
         const int g64 = (M + 63) / 64;
-        const bool eight = tuning().tokens_waves ? tuning().tokens_waves == 8
-                                                 : g64 > cus && g64 <= 2 * cus;
-        if (eight)
+        int nw = tuning().tokens_waves;
+        if (nw != 4 && nw != 6 && nw != 8) {
+            int best = 0;
+            for (const int c : {8, 6, 4}) {
+                const int groups = (M + 16 * c - 1) / (16 * c);
+                const int load = 16 * c * ((groups + cus - 1) / cus);
+                if (best == 0 || load < best) best = load, nw = c;
+            }
+        }
+        if (nw == 8)
             gemv_tokens_lds_kernel<XT, YT, 1, 8>
                 <<<(M + 127) / 128, 512, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
+        else if (nw == 6)
+            gemv_tokens_lds_kernel<XT, YT, 1, 6>
+                <<<(M + 95) / 96, 384, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
         else
             gemv_tokens_lds_kernel<XT, YT, 1, 4><<<g64, 256, 0, st>>>(y, w, x, M, n_tok, K, nullptr, nb);
         return hipGetLastError();
