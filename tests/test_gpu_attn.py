@@ -137,10 +137,13 @@ def test_decode_api_matches_c_abi():
 # (n_heads, n_kv, head_dim, N, start_pos, int8): GQA groups 1, 2 (6 heads per
 # KV head: two head blocks), 4, 8 and 32 (two blocks of 16), head_dim 64 and
 # 128 (matrix-core prefill) and 80 (VALU kernel), N not a multiple of the
-# token block, int8 with and without scales.  The last two have more
-# workgroups (8 KV heads x 33-34 blocks of 16 tokens) than the 256 CUs and
-# take the one-group kernel; the others the two-group kernel (both stage V
-# row-major and read it back with transposing LDS reads).
+# token block, int8 with and without scales.  A workgroup pairs an early
+# token half block with the mirror late one: odd half-block counts (100,
+# 520, 530 tokens at 8 tokens a half block) leave the middle one paired with
+# itself.  The last two have more workgroups (8 KV heads x 33-34 pairs of
+# 8-token half blocks) than the 256 CUs and take the one-group kernel; the
+# others the two-group kernel (both stage V row-major and read it back with
+# transposing LDS reads).
 PREFILL = [(32, 8, 128, 100, 0, False), (16, 4, 128, 300, 37, False), (8, 8, 64, 70, 5, False),
            (16, 2, 64, 33, 200, False), (32, 1, 128, 20, 10, False), (12, 2, 128, 17, 3, False),
            (16, 4, 128, 50, 64, "scales"), (8, 2, 64, 40, 0, "plain"), (4, 2, 80, 9, 4, False),
