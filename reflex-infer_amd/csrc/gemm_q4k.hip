@@ -1169,16 +1169,17 @@ static hipError_t launch_tokens_t(void *y, const uint8_t *w, const uint16_t *x, 
         // Workgroups of W = 4, 6 or 8 waves (16 rows each), one per CU when
         // they fit: W minimises the rows of the busiest CU, 16 W times the
         // rounds of workgroups (ties to the larger W).  [22016 x 2048]: 230
-        // workgroups of 96 rows (4 waves: 344 put two on 88 CUs, 8 waves:
-        // 172 leave 84 CUs idle; m = 16 13.5 / 11.8 us).
+        // workgroups of 96 rows (4 waves: 344 put two on 88 CUs; 8 waves:
+        // 172 leave 84 CUs idle); m = 16: 13.5 / 11.8 / 11.1 us with 4 / 8 /
+        // 6 waves.
         const int g64 = (M + 63) / 64;
         int nw = tuning().tokens_waves;
         if (nw != 4 && nw != 6 && nw != 8) {
             int best = 0;
             for (const int c : {8, 6, 4}) {
                 const int groups = (M + 16 * c - 1) / (16 * c);
-                const int load = 16 * c * ((groups + cus - 1) / cus);
-                if (best == 0 || load < best) best = load, nw = c;
+                const int busiest = 16 * c * ((groups + cus - 1) / cus);  // rows of the busiest CU
+                if (best == 0 || busiest < best) best = busiest, nw = c;
             }
         }
         if (nw == 8)
