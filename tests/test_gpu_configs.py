@@ -730,12 +730,15 @@ def test_prefill_gemm_mixed_token_tiles_f16():
 
 
 # ------------------------- small batch with x in LDS: super-block counts
-@pytest.mark.parametrize("M,m,K", [(16448, 12, 2816), (16384, 5, 512), (22016, 16, 4096)])
+@pytest.mark.parametrize("M,m,K", [(16448, 12, 2816), (16384, 5, 512), (22016, 16, 4096),
+                                   (32768, 7, 512)])
 def test_small_batch_lds_kernel_block_counts(M, m, K):
     """The LDS small-batch kernel (at least one 64-row workgroup per CU) on
     rows of 11, 2 and 16 super-blocks (odd counts end on a half-filled
     prefetch pair), sampled rows against the reference per-token GEMV and
-    the fp64 product of the kernel's operands."""
+    the fp64 product of the kernel's operands.  On 256 CUs the launcher
+    takes six-wave workgroups for 16448 and 22016 rows (the x tile's copies
+    repeat), four waves for 16384 and eight for 32768."""
     print(f"lds small batch [{M}x{K}] m={m}", flush=True)
     W = qweights(9200 + m, M, K)
     x16 = util.x_f16(9201 + m, (m, K))
