@@ -135,7 +135,9 @@ hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, 
 //   RXQ4_MULTI_TOKEN_GEMV=0 (2..4 tokens on the MFMA small-batch kernel),
 //   RXQ4_GEMM_TM=128|256 (the GEMM's token tile),
 //   RXQ4_GEMM_ORDER=1|2 (the GEMM's unit order: row-major | token-major),
-//   RXQ4_GEMM_NW=4|8 (the GEMM's waves per workgroup: 128- or 256-row tiles).
+//   RXQ4_GEMM_NW=4|8 (the GEMM's waves per workgroup: 128- or 256-row tiles),
+//   RXQ4_TOKENS_WAVES=4|6|8 (waves of the LDS small-batch kernel's workgroups),
+//   RXQ4_TOKENS_LDS_SPLIT=n (its K split on long rows).
 struct Tuning {
     int gemm_splits = 0;
     int gemv_waves_per_cu = 0;
