@@ -1099,6 +1099,18 @@ static hipError_t launch_gemm_tm(void *y, const uint8_t *w, const uint16_t *x, i
         }
     }
     if (tuning().gemm_mixed > 0 && T != 14) big = tuning().gemm_mixed;
+    if constexpr (T == 14) {
+        // Q6_K (128-token tiles only): the same four-wave rule as below
+        // ([2048 x 11008] at m = 512: 49.1 -> 45.5 us on one box)
+        int nw = tuning().gemm_nw;
+        if (nw != 4 && nw != 8) {
+            const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
+            const int64_t tiles8 = (int64_t)((M + kRowsPerWg - 1) / kRowsPerWg) * ((N + 127) / 128);
+            const int64_t splits8 = std::min<int64_t>(cus / std::max<int64_t>(1, tiles8), (K / 256) / 2);
+            nw = splits8 >= 8 ? 4 : 8;
+        }
+        if (nw == 4) return launch_gemm_t<T, XT, YT, 128, 4>(y, w, x, M, N, K, st, sc);
+    }
     if constexpr (T != 14) {
         // Four-wave workgroups (128-row tiles, one wave per SIMD) for shapes
         // that the eight-wave plan splits 8 ways or more: twice the tiles

@@ -152,8 +152,9 @@ def test_q6k_embedding_bit_exact(K):
 
 @pytest.mark.parametrize("t", [13, 14])
 # up to 16 tokens: the small-batch kernel (row tiles of 16 and 32); more:
-# the eight-wave MFMA GEMM (partial row and token tiles, split K at 64 rows;
-# K = 11008 and 2304 give Q6_K rows that start on odd 2-byte boundaries)
+# the MFMA GEMM (partial row and token tiles; the 64- and 40-row shapes split
+# K 8 ways or more and take the four-wave workgroups; K = 11008 and 2304
+# give Q6_K rows that start on odd 2-byte boundaries)
 @pytest.mark.parametrize("M,N,K", [(300, 2, 2048), (129, 17, 512), (64, 40, 11008), (33, 5, 256),
                                    (600, 130, 1024), (2100, 70, 512), (1000, 300, 2304),
                                    (96, 40, 256), (40, 24, 65536)])
