@@ -507,7 +507,12 @@ static hipError_t launch_kq_gemv_p(const KqGemvParams &p, hipStream_t st) {
     const size_t lds = (size_t)p.K * 2 + (size_t)(p.K / 16) * 4;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-    const int wg_per_cu = (int)std::max<size_t>(1, std::min<size_t>(4, (160 * 1024) / lds));
+    // at most 3 workgroups (12 waves) per CU: the Q6_K LM head [151936 x
+    // 2048] took 50.1-51.0 us with 3, 53.8-54.0 with 4, 55.6-57.1 with 5-6
+    // and 58.5 with 2 (alternating runs on one box); down (one wave per row,
+    // 512 workgroups) is below every cap
+    constexpr size_t kWgPerCu = 3;
+    const int wg_per_cu = (int)std::max<size_t>(1, std::min<size_t>(kWgPerCu, (160 * 1024) / lds));
     const int want = (p.n_units + 3) / 4;
     const int grid = std::max(1, std::min(want, cus * wg_per_cu));
     if (lds > 64 * 1024) {
