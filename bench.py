@@ -577,7 +577,7 @@ def main() -> int:
 
         # Q6_K (ggml type 14): LM head, embedding gather and ffn_down as a
         # Q4_K_M file stores them, and the Qwen3-4B-style mixed QKV triple
-        # (Q4_K q, k + Q6_K v).  Random blocks with a fixed d (timing only).
+        # (Q4_K q, k + Q6_K v), on weights from ggml's reference quantiser.
         def q6_blocks(seed, rows, K):
             return qweights(seed, rows, K, ggml_type=14)
 
