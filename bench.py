@@ -134,6 +134,8 @@ LEGS = {
     "gate_up_m16": (12, 2 * FFN, HIDDEN, 16, "tokens"),
     "down_m16": (12, HIDDEN, FFN, 16, "tokens"),
     "attn_prefill": (0, 0, 0, 512, "attn_prefill"),
+    "q6k_lm_head": (14, VOCAB, HIDDEN, 1, "f32"),
+    "q6k_gemm512_2048x11008": (14, HIDDEN, FFN, 512, "gemm"),
 }
 
 
@@ -179,29 +181,29 @@ def run_leg(name: str, graph: bool = False) -> int:
         ids = torch.from_numpy(rng.permutation(VOCAB)[np.minimum(
             np.searchsorted(cdf, rng.random(m)), VOCAB - 1)].astype(np.int32)).to(dev)
         out = torch.empty((m, K), dtype=torch.float16, device=dev)
-        run = lambda i: capi.embed_rows_f16(out, ws[i % n_copies], VOCAB, ids, K)  # noqa: E731
+        run = lambda i: capi.embed_rows_f16(out, ws[i % n_copies], VOCAB, ids, K, ggml_type=t)  # noqa: E731
     elif kind == "gemm":
         xb = gen(1, (m, K), 1.0).to(torch.bfloat16)
         yb = torch.empty((m, M), dtype=torch.bfloat16, device=dev)
-        run = lambda i: capi.gemm(yb, ws[i % n_copies], xb, M, m, K)  # noqa: E731
+        run = lambda i: capi.gemm(yb, ws[i % n_copies], xb, M, m, K, ggml_type=t)  # noqa: E731
     elif kind == "tokens":
         xt = gen(4, (m, K), 1.0).half()
         yt = torch.empty((m, M), dtype=torch.float16, device=dev)
-        run = lambda i: capi.gemm_f16(yt, ws[i % n_copies], xt, M, m, K)  # noqa: E731
+        run = lambda i: capi.gemm_f16(yt, ws[i % n_copies], xt, M, m, K, ggml_type=t)  # noqa: E731
     else:
         x = gen(2, (K,), 1.0).half()
         if kind == "f32":
             y = torch.empty(M, dtype=torch.float32, device=dev)
-            run = lambda i: capi.gemv_f32(y, ws[i % n_copies], x, M, K)  # noqa: E731
+            run = lambda i: capi.gemv_f32(y, ws[i % n_copies], x, M, K, ggml_type=t)  # noqa: E731
         elif kind == "add":
             y = torch.empty(M, dtype=torch.float16, device=dev)
             res = gen(3, (M,), 1.0).half()
-            run = lambda i: capi.gemv_add_f16(y, ws[i % n_copies], x, res, M, K)  # noqa: E731
+            run = lambda i: capi.gemv_add_f16(y, ws[i % n_copies], x, res, M, K, ggml_type=t)  # noqa: E731
         else:
             y = torch.empty(M, dtype=torch.float16, device=dev)
             h = M // 2
             run = lambda i: capi.gemv_multi_f16(  # noqa: E731
-                [(y[:h], ws[i % n_copies][:h], h), (y[h:], ws[i % n_copies][h:], h)], x, K)
+                [(y[:h], ws[i % n_copies][:h], h, t), (y[h:], ws[i % n_copies][h:], h, t)], x, K)
     torch.cuda.synchronize()
     if not graph:
         for i in range(launches):
