@@ -546,6 +546,54 @@ def test_prefill_gemm_four_wave_workgroups(tm):
     assert "four-wave ok" in r.stdout
 
 
+KQ_FORCED_GEMM = r"""
+import sys, numpy as np, torch
+sys.path[:0] = [ROOT, ROOT + "/reflex-infer_amd"]
+import rxq4
+from rxq4 import capi
+from oracle import oracle as orc
+from tests import kquant_blocks as kb, util
+# (M, N, K): partial last row and token tiles, one super-block per row, a
+# last token tile of one token, long rows split 8 ways or more (the shapes
+# that take four-wave workgroups by themselves), Q6_K rows that start on odd
+# 2-byte boundaries (K = 2304, 11008)
+CASES = [(300, 100, 11008), (264, 130, 512), (520, 129, 256), (250, 40, 2304),
+         (129, 33, 512), (64, 17, 11008)]
+for t in (13, 14):
+    for M, N, K in CASES:
+        print("forced gemm type", t, M, N, K, flush=True)
+        Wn = kb.random_blocks(t, util.rng(9400 + t + M), M, K)
+        W = torch.from_numpy(Wn).cuda()
+        xb = util.f32_to_bf16_bits(util.gaussian(9401 + N, (N, K)))
+        x = torch.from_numpy(xb.view(np.int16)).cuda().view(torch.bfloat16)
+        rows = np.sort(util.rng(9402).choice(M, min(M, 96), replace=False))
+        ref = orc.kq_gemm_f64(np.ascontiguousarray(Wn[rows]), K, t,
+                              orc.bits_bf16_to_f32(xb), "bf16")
+        y = torch.empty((N, M), dtype=torch.float32, device="cuda")
+        capi.gemm(y, W, x, M, N, K, ggml_type=t)
+        assert util.rel_err(y.cpu().numpy()[:, rows], ref) <= util.TOL, (t, M, N, K)
+        yb = torch.empty((N, M), dtype=torch.bfloat16, device="cuda")
+        capi.gemm(yb, W, x, M, N, K, ggml_type=t)
+        got = yb.view(torch.int16).cpu().numpy().view(np.uint16)[:, rows]
+        assert util.rounded_ok(got, ref, "bf16").all(), (t, M, N, K)
+print("forced ok", flush=True)
+"""
+
+
+@pytest.mark.parametrize("nw,tm", [("4", "128"), ("4", "256"), ("8", "128")])
+def test_kq_gemm_forced_workgroups(nw, tm):
+    """Q5_K and Q6_K GEMMs with the four- or eight-wave workgroup forced for
+    every shape (Q6_K takes 128-token tiles whatever the token tile asked
+    for): sampled rows against the fp64 oracle on the bf16-rounded weights.
+    By themselves the launchers take four waves only for shapes split 8
+    ways or more."""
+    env = dict(os.environ, RXQ4_GEMM_NW=nw, RXQ4_GEMM_TM=tm)
+    r = subprocess.run([sys.executable, "-c", KQ_FORCED_GEMM.replace("ROOT", repr(ROOT))],
+                       env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-1500:] + r.stderr[-3000:]
+    assert "forced ok" in r.stdout
+
+
 # --------------------------------------------------- very long rows, m <= 4
 @pytest.mark.parametrize("M,N,K", [(64, 4, 28672), (64, 3, 24320), (64, 2, 65536),
                                    (64, 4, 16384)])

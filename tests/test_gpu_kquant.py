@@ -39,8 +39,9 @@ def f16(bits: np.ndarray) -> np.ndarray:
 # (rows, K): packed rows per wave step (K 2048 -> 2 rows, 256 -> 16 rows,
 # 4096 -> 1 row), long rows (11008: 172 slots, 1536: 24 slots), a partial last
 # step (37 rows), and a K whose x staging needs more than 64 KiB of LDS.
-# 70001 x 2048 gives each of the 4096 waves 8-9 packed steps (the pipelined
-# steady state, an odd last step and a reload past the end).
+# 70001 x 2048 gives each of the 3072 waves (three four-wave workgroups per
+# CU) 11-12 packed steps (the pipelined steady state, an odd last step and a
+# reload past the end).
 GEMV_SHAPES = [(256, 2048), (300, 256), (37, 4096), (100, 11008), (64, 1536), (3, 32768),
                (70001, 2048)]
 
