@@ -29,6 +29,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
+#include <type_traits>
 
 namespace rxq4 {
 
@@ -425,6 +427,168 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Streamed register kernel (one token, the register kernel's lane mapping
+// and arithmetic), for waves of many steps (long matrices such as the LM
+// head).  A step of a wave is 64 slots = 16 blocks = 2304 contiguous bytes,
+// and a wave's steps are contiguous, so a group of 3 steps (6912 B) arrives
+// by 7 direct-to-LDS 16-byte loads per lane, each covering up to 1 KB
+// contiguous (whole 128-byte lines, marked nontemporal), into a per-wave
+// double buffer in LDS; each lane then reads its slot's header and quants
+// from there.  Loads past the group, past the wave's last step or past the
+// range take an offset beyond the buffer resource (no memory access, zeros
+// into LDS), so a wave reads exactly its own rows and every load is issued
+// unconditionally (exact vmcnt waits).
+// Measured on the Q4_K LM head [151936 x 2048] (graph replay, alternating
+// runs on one box): 33.5 us for the register kernel; streamed 30.1-30.5
+// with 3-step groups x 2 buffers, 30.2-30.6 with 2 x 3, 31.0-31.4 with 2 x 4
+// or 4 x 2 (18 KB in flight), 31.4-32.0 with 2 x 2, 32.0-33.0 with 1-step
+// groups; without the nontemporal bit 35.2-35.5; 31.2-31.4 with 8 waves per
+// CU.  Waves of 11 steps (gate+up) ran 6% slower streamed: the first
+// group's round trip is longer than the register kernel's first step.
+constexpr int kStepBytes = 64 * 36;
+constexpr int kStreamSteps = 3;
+constexpr int kStreamGroupBytes = kStreamSteps * kStepBytes;
+constexpr int kStreamLoads = (kStreamGroupBytes + 1023) / 1024;
+constexpr int kStreamBufBytes = kStreamLoads * 1024;  // a group's LDS buffer
+constexpr int kStreamBufs = 2;
+// dynamic LDS per workgroup (4 waves)
+constexpr size_t kStreamLds = (size_t)4 * kStreamBufs * kStreamBufBytes;
+// waves of at least this many steps take the streamed kernel
+constexpr int kStreamMinSteps = 32;
+
+// f(integral_constant<int, I>) for I = B .. E-1, unrolled.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+template <int LPR, int EPI, int NBUF>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
+    constexpr int RPS = 64 / LPR;
+    extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
+    __shared__ __attribute__((aligned(16))) uint16_t xsh[kRegMaxK];
+    __shared__ float outs[4][kRegMaxRows];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = blockIdx.x * 4 + wv;
+    const bool active = wave < p.total_units;
+    const Range rg = range_of_unit(p, active ? wave : 0);
+    const int n_steps = (rg.rows + RPS - 1) / RPS;
+    const int t0 = active ? (wave - rg.first_unit) * p.per_unit : 0;
+    const int t1 = active ? min(t0 + p.per_unit, n_steps) : 0;
+    const int row0 = t0 * RPS;
+    const int last = rg.rows - 1;
+    const int slot = lane & (LPR - 1);
+    const int sub = lane / LPR;
+    const int il = slot & 3;
+    const int b = slot >> 2;
+
+    const int x_bytes = p.nb * kQK * 2;
+    const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(p.x, x_bytes);
+    constexpr int kXRounds = (RPS == 1) ? 2 : 1;
+#pragma unroll
+    for (int r = 0; r < kXRounds; ++r)
+        buffer_to_lds16(xrsrc, &xsh[(256 * r + 64 * wv) * 8], (256 * r + tid) * 16);
+    uint32_t res = 0;
+    if (EPI == kEpiAdd) res = rg.res[min(row0 + lane, last)];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // The range's bytes (the host checks that they fit a buffer resource);
+    // the wave's own bytes end at step t1.
+    const uint32_t row_bytes = (uint32_t)p.nb * kBlockBytes;
+    const __amdgpu_buffer_rsrc_t wrsrc = make_rsrc(rg.w, (int)((uint32_t)rg.rows * row_bytes));
+    const int end = t1 * kStepBytes;
+    uint8_t *my = ring + wv * (NBUF * kStreamBufBytes);
+    const int n = t1 - t0;
+    const int n_groups = (n + kStreamSteps - 1) / kStreamSteps;
+    auto load = [&](int g, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kStreamLoads; ++j) {
+            const int off = (t0 * kStepBytes + g * kStreamGroupBytes) + j * 1024 + lane * 16;
+            const bool mine = j * 1024 + lane * 16 < kStreamGroupBytes && off < end;
+            buffer_to_lds16_nt(wrsrc, my + buf * kStreamBufBytes + j * 1024,
+                               mine ? off : 0x7FFFFFF0);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i) load(i, i);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<NBUF * kStreamLoads>();  // this wave's x copies (and residual) have landed
+    lds_barrier();                      // ... and every other wave's
+
+    XSlot xs;
+    {
+        u32x4 xraw[8];
+        const u32x4 *xs16 = reinterpret_cast<const u32x4 *>(xsh) + b * 32 + il * 8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xraw[i] = xs16[i];
+        x_slot_from_raw(xraw, xs);
+    }
+    const ScaleDecode sd = scale_decode_for(il);
+    const uint32_t magic = magic_vgpr();
+    // lane's slot in a step: block lane / 4 of the step, quant group lane & 3
+    const int hdr_lds = (lane >> 2) * kBlockBytes;
+    const int q_lds = hdr_lds + 16 + 32 * (lane & 3);
+    // One group: its 3 LDS reads per step all first (a lone wave on its SIMD
+    // would otherwise wait out the LDS latency per step), then the steps;
+    // `full` groups (all steps the wave's) skip the per-step test.
+    auto compute = [&](int g, int buf, auto full) __attribute__((always_inline)) {
+        const uint8_t *gb = my + buf * kStreamBufBytes;
+        u32x4 h[kStreamSteps], q0[kStreamSteps], q1[kStreamSteps];
+#pragma unroll
+        for (int s = 0; s < kStreamSteps; ++s) {
+            const uint8_t *sb = gb + s * kStepBytes;
+            h[s] = *reinterpret_cast<const u32x4 *>(sb + hdr_lds);
+            q0[s] = *reinterpret_cast<const u32x4 *>(sb + q_lds);
+            q1[s] = *reinterpret_cast<const u32x4 *>(sb + q_lds + 16);
+        }
+#pragma unroll
+        for (int s = 0; s < kStreamSteps; ++s) {
+            const int t = g * kStreamSteps + s;
+            if (decltype(full)::value || t < n) {  // uniform
+                const float r = lane_group_sum<LPR>(slot_dot(h[s], q0[s], q1[s], xs, sd, magic));
+                if (slot == LPR - 1) outs[wv][t * RPS + sub] = r;
+            }
+        }
+    };
+    using Full = std::integral_constant<bool, true>;
+    using Tail = std::integral_constant<bool, false>;
+
+    // Steady state: groups g .. g+NBUF-1 in flight, group g+i in buffer i;
+    // each buffer is refilled once its group has been read (the reads'
+    // values are used before the refill is issued).  The tail computes the
+    // last NBUF groups with no loads behind them.
+    int g = 0;
+    for (; g + NBUF < n_groups; g += NBUF) {
+        static_for<0, NBUF>([&](auto i) __attribute__((always_inline)) {
+            constexpr int I = decltype(i)::value;
+            wait_vmcnt<(NBUF - 1) * kStreamLoads>();
+            compute(g + I, I, Full{});
+            __builtin_amdgcn_sched_barrier(0);
+            load(g + I + NBUF, I);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    static_for<0, NBUF>([&](auto i) __attribute__((always_inline)) {
+        constexpr int I = decltype(i)::value;
+        wait_vmcnt<(NBUF - 1 - I) * kStreamLoads>();
+        compute(g + I, I, Tail{});
+    });
+
+    const int rows = min(n * RPS, rg.rows - row0);
+    if (lane < rows) store_row<EPI>(rg, row0 + lane, outs[wv][lane], res);
+    for (int r = 64; r < rows; r += 64) {
+        const int row = row0 + r + lane;
+        if (r + lane < rows)
+            store_row<EPI>(rg, row, outs[wv][r + lane], EPI == kEpiAdd ? rg.res[row] : 0u);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // LDS kernel for rows with more than 64 slots (any K): the workgroup stages
 // x once in LDS in the same permuted-pair layout (36 dwords per slot), and
 // each wave owns whole rows, walking a row's slots 64 at a time
@@ -613,9 +777,44 @@ static int assign_units(GemvParams &p, int rows_per_item, int per_unit) {
 #endif
 constexpr int kRegBatch = RXQ4_GEMV_BATCH;
 
+
+// Whether every range of a one-token launch fits a buffer resource with room
+// for the streamed kernel's out-of-range offset.
+static bool stream_fits(const GemvParams &p) {
+    const int64_t row_bytes = (int64_t)p.nb * kBlockBytes;
+    for (int i = 0; i < p.n_ranges; ++i)
+        if ((int64_t)p.r[i].rows * row_bytes > 0x7FFF0000LL) return false;
+    return true;
+}
+
+template <int LPR, int EPI>
+static hipError_t launch_stream(const GemvParams &p, int grid, hipStream_t st) {
+    // the dynamic LDS limit, raised once per device (devices 0..63)
+    static std::atomic<uint64_t> raised{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(raised.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_stream_kernel<LPR, EPI, kStreamBufs>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStreamLds);
+        if (e != hipSuccess) return e;
+        raised.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    gemv_stream_kernel<LPR, EPI, kStreamBufs><<<grid, 256, kStreamLds, st>>>(p);
+    return hipSuccess;
+}
+
 template <int LPR, int EPI, int NT>
-static void launch_reg(const GemvParams &p, int grid, hipStream_t st) {
+static hipError_t launch_reg(const GemvParams &p, int grid, hipStream_t st) {
+    // RXQ4_GEMV_STREAM: 0 never, n > 0 from n steps per wave
+    const int min_steps = tuning().gemv_stream < 0   ? INT32_MAX
+                          : tuning().gemv_stream > 0 ? tuning().gemv_stream
+                                                     : kStreamMinSteps;
+    if (NT == 1 && p.per_unit >= min_steps && stream_fits(p))
+        return launch_stream<LPR, EPI>(p, grid, st);
     gemv_reg_kernel<LPR, EPI, kRegBatch, NT><<<grid, 256, 0, st>>>(p);
+    return hipSuccess;
 }
 
 template <int EPI, int NT>
@@ -631,13 +830,15 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         per_wave = std::max(1, std::min(per_wave, kRegMaxRows / rps));
         const int waves = assign_units(p, rps, per_wave);
         const int grid = (waves + 3) / 4;
+        hipError_t e;
         switch (slots) {
-            case 4: launch_reg<4, EPI, NT>(p, grid, st); break;
-            case 8: launch_reg<8, EPI, NT>(p, grid, st); break;
-            case 16: launch_reg<16, EPI, NT>(p, grid, st); break;
-            case 32: launch_reg<32, EPI, NT>(p, grid, st); break;
-            default: launch_reg<64, EPI, NT>(p, grid, st); break;
+            case 4: e = launch_reg<4, EPI, NT>(p, grid, st); break;
+            case 8: e = launch_reg<8, EPI, NT>(p, grid, st); break;
+            case 16: e = launch_reg<16, EPI, NT>(p, grid, st); break;
+            case 32: e = launch_reg<32, EPI, NT>(p, grid, st); break;
+            default: e = launch_reg<64, EPI, NT>(p, grid, st); break;
         }
+        if (e != hipSuccess) return e;
     } else {
         // LDS kernel: whole rows per wave, `waves_per_cu` waves per CU.
         const size_t lds = (size_t)NT * slots * kLdsSlotWords * sizeof(uint32_t);

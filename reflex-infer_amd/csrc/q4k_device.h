@@ -131,6 +131,14 @@ __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rsrc, voi
         rsrc, (void __attribute__((address_space(3))) *)lds, 16, voffset, soffset, 0, 0);
 }
 
+// buffer_to_lds16 marked nontemporal (cache policy 2 = nt), for data read
+// once: a stream whose every load instruction covers whole 128-byte lines.
+__device__ __forceinline__ void buffer_to_lds16_nt(__amdgpu_buffer_rsrc_t rsrc, void *lds,
+                                                   int voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rsrc, (void __attribute__((address_space(3))) *)lds, 16, voffset, 0, 0, 2);
+}
+
 // s_waitcnt lgkmcnt(0) (vmcnt and expcnt untouched).
 __device__ __forceinline__ void wait_lgkmcnt0() {
     __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));

@@ -123,6 +123,7 @@ const Tuning &tuning() {
         r.tokens_waves = env_pos("RXQ4_TOKENS_WAVES");
         r.tokens_lds_split = env_pos("RXQ4_TOKENS_LDS_SPLIT");
         r.gemm_nw = env_pos("RXQ4_GEMM_NW");
+        r.gemv_stream = env_off("RXQ4_GEMV_STREAM") ? -1 : env_pos("RXQ4_GEMV_STREAM");
         return r;
     }();
     return t;

@@ -546,6 +546,87 @@ def test_prefill_gemm_four_wave_workgroups(tm):
     assert "four-wave ok" in r.stdout
 
 
+STREAM_GEMV = r"""
+import hashlib, sys, numpy as np, torch
+sys.path[:0] = [ROOT, ROOT + "/reflex-infer_amd"]
+import rxq4
+from rxq4 import capi
+from oracle import oracle as orc
+from tests import util
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    return torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).cuda()
+
+def host16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+def digest(t):
+    torch.cuda.synchronize()
+    return hashlib.sha1(t.cpu().numpy().tobytes()).hexdigest()[:12]
+
+# (M, K): every register-kernel row length (K 256 .. 4096: 16 .. 1 rows a
+# step), one partial step, waves with a loop pass and a partial last group
+# (40000 x 1024: 10 steps a wave), and more rows than a buffer resource of
+# one wave's group
+CASES = [(7, 256), (33, 512), (129, 1024), (2051, 2048), (301, 4096), (40000, 1024),
+         (70001, 2048)]
+for M, K in CASES:
+    print("streamed gemv", M, K, flush=True)
+    Wn = util.weights(9500 + M, M, K)
+    x16, res16 = util.x_f16(9501 + K, K), util.x_f16(9502, M)
+    ref = orc.gemv_f32(Wn, K, x16)
+    W, x, res = dev(Wn), dev(x16), dev(res16)
+    y32 = torch.empty(M, dtype=torch.float32, device="cuda")
+    capi.gemv_f32(y32, W, x, M, K)
+    assert util.rel_err(y32.cpu().numpy(), ref) <= util.TOL, (M, K)
+    y16 = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_f16(y16, W, x, M, K)
+    assert util.rounded_ok(host16(y16), ref).all(), (M, K)
+    ya = torch.empty(M, dtype=torch.float16, device="cuda")
+    capi.gemv_add_f16(ya, W, x, res, M, K)
+    assert util.rel_err(ya.float().cpu().numpy(),
+                        orc.gemv_add_f16(Wn, K, x16, res16).view(np.float16).astype(np.float32)) <= util.TOL
+    # in place: y is the residual
+    capi.gemv_add_f16(res, W, x, res, M, K)
+    assert torch.equal(res, ya.view(torch.int16)), (M, K)  # res holds fp16 bits as int16
+    print("DIGEST", M, K, digest(y32), digest(y16), digest(ya), flush=True)
+# a pair and a triple (ranges of 11008 + 3 rows, 2048 + 256 + 256 rows)
+K = 2048
+x16 = util.x_f16(9510, K)
+x = dev(x16)
+for Ms in ((11008, 3), (2048, 256, 256)):
+    print("streamed multi", Ms, flush=True)
+    Wn = [util.weights(9511 + i, m, K) for i, m in enumerate(Ms)]
+    Wd = [dev(w) for w in Wn]
+    ys = [torch.empty(m, dtype=torch.float16, device="cuda") for m in Ms]
+    capi.gemv_multi_f16([(y, w, m) for y, w, m in zip(ys, Wd, Ms)], x, K)
+    for y, w in zip(ys, Wn):
+        assert util.rounded_ok(host16(y), orc.gemv_f32(w, K, x16)).all(), Ms
+    print("DIGEST", Ms, *[digest(y) for y in ys], flush=True)
+print("stream ok", flush=True)
+"""
+
+
+def test_gemv_streamed_kernel_forced():
+    """The one-token GEMV streamed through LDS (RXQ4_GEMV_STREAM=1: every
+    register-kernel launch; by default only waves of 32 steps or more, e.g.
+    the LM head) against the oracle, f32 / f16 / add (in place too), pair
+    and triple; RXQ4_GEMV_STREAM=0 runs the same cases on the register
+    kernel, and the two runs' outputs must be byte-identical (same
+    arithmetic)."""
+    digests = {}
+    for mode in ("1", "0"):
+        env = dict(os.environ, RXQ4_GEMV_STREAM=mode)
+        r = subprocess.run([sys.executable, "-c", STREAM_GEMV.replace("ROOT", repr(ROOT))],
+                           env=env, capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, mode + r.stdout[-1500:] + r.stderr[-3000:]
+        assert "stream ok" in r.stdout
+        digests[mode] = [l for l in r.stdout.splitlines() if l.startswith("DIGEST")]
+    assert len(digests["1"]) == 9
+    assert digests["1"] == digests["0"]
+
+
 KQ_FORCED_GEMM = r"""
 import sys, numpy as np, torch
 sys.path[:0] = [ROOT, ROOT + "/reflex-infer_amd"]
