@@ -428,33 +428,44 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 
 // ---------------------------------------------------------------------------
 // Streamed register kernel (one token, the register kernel's lane mapping
-// and arithmetic), for waves of many steps (long matrices such as the LM
-// head).  A step of a wave is 64 slots = 16 blocks = 2304 contiguous bytes,
-// and a wave's steps are contiguous, so a group of 3 steps (6912 B) arrives
-// by 7 direct-to-LDS 16-byte loads per lane, each covering up to 1 KB
-// contiguous (whole 128-byte lines, marked nontemporal), into a per-wave
-// double buffer in LDS; each lane then reads its slot's header and quants
-// from there.  Loads past the group, past the wave's last step or past the
-// range take an offset beyond the buffer resource (no memory access, zeros
-// into LDS), so a wave reads exactly its own rows and every load is issued
-// unconditionally (exact vmcnt waits).
-// Measured on the Q4_K LM head [151936 x 2048] (graph replay, alternating
-// runs on one box): 33.5 us for the register kernel; streamed 30.1-30.5
-// with 3-step groups x 2 buffers, 30.2-30.6 with 2 x 3, 31.0-31.4 with 2 x 4
-// or 4 x 2 (18 KB in flight), 31.4-32.0 with 2 x 2, 32.0-33.0 with 1-step
-// groups; without the nontemporal bit 35.2-35.5; 31.2-31.4 with 8 waves per
-// CU.  Waves of 11 steps (gate+up) ran 6% slower streamed: the first
-// group's round trip is longer than the register kernel's first step.
+// and arithmetic).  A step of a wave is 64 slots = 16 blocks = 2304
+// contiguous bytes, and a wave's steps are contiguous, so a group of G steps
+// arrives by ceil(G * 2304 / 1024) direct-to-LDS 16-byte loads per lane,
+// each covering up to 1 KB contiguous (whole 128-byte lines, marked
+// nontemporal), into a per-wave ring of NBUF group buffers in LDS; each lane
+// then reads its slot's header and quants from there.  Loads past the group,
+// past the wave's last step or past the range take an offset beyond the
+// buffer resource (no memory access, zeros into LDS), so a wave reads
+// exactly its own rows and every load is issued unconditionally (exact
+// vmcnt waits).  Against the register kernel (graph replay, alternating
+// runs on one box, identical outputs):
+//   * waves of 32 steps or more (the LM head [151936 x 2048], 74 steps):
+//     3-step groups x 2 buffers, 33.5 -> 30.1-30.5 us; 2 x 3 30.2-30.6,
+//     2 x 4 or 4 x 2 (18 KB in flight) 31.0-31.4, 2 x 2 31.4-32.0, 1-step
+//     groups 32.0-33.0; without the nontemporal bit 35.2-35.5; with 8 waves
+//     per CU 31.2-31.4; groups dealt round-robin over the range's waves
+//     (rows stored per step) 35.6-37.2;
+//   * shorter waves: 1-step groups x 3 buffers, QKV triple 3.36 -> 2.82,
+//     O add 3.19 -> 2.60, gate+up pair 6.85 -> 6.59 us (x 2 buffers: 2.79,
+//     2.57, 7.70; 1 x 4: 2.87, 2.71, 6.54; 3 x 2: gate+up 7.2; 6 or 8
+//     waves per CU slower on QKV).
 constexpr int kStepBytes = 64 * 36;
-constexpr int kStreamSteps = 3;
-constexpr int kStreamGroupBytes = kStreamSteps * kStepBytes;
-constexpr int kStreamLoads = (kStreamGroupBytes + 1023) / 1024;
-constexpr int kStreamBufBytes = kStreamLoads * 1024;  // a group's LDS buffer
-constexpr int kStreamBufs = 2;
-// dynamic LDS per workgroup (4 waves)
-constexpr size_t kStreamLds = (size_t)4 * kStreamBufs * kStreamBufBytes;
-// waves of at least this many steps take the streamed kernel
+// waves of at least this many steps take the long-group configuration
 constexpr int kStreamMinSteps = 32;
+constexpr int kStreamLongSteps = 3, kStreamLongBufs = 2;
+constexpr int kStreamShortSteps = 1, kStreamShortBufs = 3;
+
+template <int G>
+struct StreamGeometry {
+    static constexpr int kGroupBytes = G * kStepBytes;
+    static constexpr int kLoads = (kGroupBytes + 1023) / 1024;
+    static constexpr int kBufBytes = kLoads * 1024;  // a group's LDS buffer
+};
+// dynamic LDS per workgroup (4 waves)
+template <int G, int NBUF>
+constexpr size_t stream_lds() {
+    return (size_t)4 * NBUF * StreamGeometry<G>::kBufBytes;
+}
 
 // f(integral_constant<int, I>) for I = B .. E-1, unrolled.
 template <int B, int E, typename F>
@@ -465,9 +476,13 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-template <int LPR, int EPI, int NBUF>
+template <int LPR, int EPI, int G, int NBUF>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     constexpr int RPS = 64 / LPR;
+    constexpr int kStreamSteps = G;
+    constexpr int kStreamGroupBytes = StreamGeometry<G>::kGroupBytes;
+    constexpr int kStreamLoads = StreamGeometry<G>::kLoads;
+    constexpr int kStreamBufBytes = StreamGeometry<G>::kBufBytes;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
     __shared__ __attribute__((aligned(16))) uint16_t xsh[kRegMaxK];
     __shared__ float outs[4][kRegMaxRows];
@@ -736,6 +751,139 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvParams p) {
     compute(B);
 }
 
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 16].
+__device__ __forceinline__ void wait_vmcnt_upto16(int n) {
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;
+        case 7: wait_vmcnt<7>(); break;
+        case 8: wait_vmcnt<8>(); break;
+        case 9: wait_vmcnt<9>(); break;
+        case 10: wait_vmcnt<10>(); break;
+        case 11: wait_vmcnt<11>(); break;
+        case 12: wait_vmcnt<12>(); break;
+        case 13: wait_vmcnt<13>(); break;
+        case 14: wait_vmcnt<14>(); break;
+        case 15: wait_vmcnt<15>(); break;
+        default: wait_vmcnt<16>(); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Streamed LDS kernel (one token, rows of more than 64 slots, the LDS
+// kernel's lane mapping and arithmetic), for waves whose rows fit 16 KB
+// (down [2048 x 11008]: 2 rows of 6192 B).  A wave's rows are contiguous,
+// so all of its weight bytes arrive by 16 unconditional direct-to-LDS
+// 16-byte loads per lane (each covering 1 KB contiguous, marked
+// nontemporal; loads past the wave's rows take an offset beyond the buffer
+// resource), issued before x is staged; each row waits only for the loads
+// that hold it, then reads its slots from LDS.  The residuals (kEpiAdd) of
+// the wave's rows are prefetched one per lane.
+constexpr int kLdsStreamWaveBytes = 16384;  // largest per-wave buffer
+
+template <int EPI, int WB>
+__global__ __launch_bounds__(256) void gemv_lds_stream_kernel(GemvParams p) {
+    static_assert(WB % 1024 == 0 && WB <= kLdsStreamWaveBytes, "whole 1 KB loads, at most 16");
+    constexpr int kLdsStreamLoads = WB / 1024;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int n_slots = 4 * p.nb;
+    const int J = (n_slots + 63) / 64;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = blockIdx.x * 4 + wv;
+    const bool active = wave < p.total_units;
+    const Range rg = range_of_unit(p, active ? wave : 0);
+    const int r0 = active ? (wave - rg.first_unit) * p.per_unit : 0;
+    const int r1 = active ? min(r0 + p.per_unit, rg.rows) : 0;
+    const int n_rows = r1 - r0;
+    const uint32_t row_bytes = (uint32_t)p.nb * kBlockBytes;
+    uint8_t *ring = smem + wv * WB;
+    uint32_t *xlds = reinterpret_cast<uint32_t *>(smem + 4 * WB);
+
+    // x, first round (slot tid), and the residuals of the wave's rows
+    const int s_first = tid;
+    const int s_load = min(s_first, n_slots - 1);
+    u32x4 xraw[8];
+    load_x_raw(p.x, s_load >> 2, s_load & 3, xraw);
+    uint32_t res = 0;
+    if (EPI == kEpiAdd) res = rg.res[min(r0 + min(lane, max(n_rows - 1, 0)), rg.rows - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    // the wave's weight bytes [r0, r1) x row_bytes (the host checks that the
+    // range fits a buffer resource and the rows 16 KB)
+    const __amdgpu_buffer_rsrc_t wrsrc = make_rsrc(rg.w, (int)((uint32_t)rg.rows * row_bytes));
+    const int wbeg = r0 * (int)row_bytes, wend = r1 * (int)row_bytes;
+#pragma unroll
+    for (int j = 0; j < kLdsStreamLoads; ++j) {
+        const int off = wbeg + j * 1024 + lane * 16;
+        buffer_to_lds16_nt(wrsrc, ring + j * 1024, off < wend ? off : 0x7FFFFFF0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    auto stage = [&](int s, const u32x4 raw[8]) {
+        XSlot xs;
+        x_slot_from_raw(raw, xs);
+        uint32_t *dst = xlds + s * kLdsSlotWords;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            *reinterpret_cast<u32x4 *>(dst + 4 * k) =
+                u32x4{xs.p[4 * k], xs.p[4 * k + 1], xs.p[4 * k + 2], xs.p[4 * k + 3]};
+        *reinterpret_cast<f32x4v *>(dst + 32) = f32x4v{xs.bias_lo, xs.bias_hi, xs.sx_lo, xs.sx_hi};
+    };
+    if (s_first < n_slots) stage(s_first, xraw);
+    for (int s = s_first + blockDim.x; s < n_slots; s += blockDim.x) {
+        load_x_raw(p.x, s >> 2, s & 3, xraw);
+        stage(s, xraw);
+    }
+    // the staged x is visible to every wave; no wait on the weight loads
+    // here (__syncthreads would wait for them: its fence counts the loads
+    // into LDS), each wave waits for its own below
+    wait_lgkmcnt0();
+    lds_barrier();
+    if (n_rows <= 0) return;
+
+    const uint32_t magic = magic_vgpr();
+    for (int k = 0; k < n_rows; ++k) {  // uniform
+        const uint8_t *rowp = ring + k * row_bytes;
+        float acc = 0.0f;
+        for (int j = 0; j < J; ++j) {
+            // item j of row k ends at byte k * row_bytes + min(64 (j+1), n_slots) / 4
+            // blocks: the first `need` loads hold it
+            const uint32_t item_end = (uint32_t)k * row_bytes + (uint32_t)min(16 * (j + 1), p.nb) * kBlockBytes;
+            wait_vmcnt_upto16(kLdsStreamLoads - min(kLdsStreamLoads, (int)((item_end + 1023) / 1024)));
+            const int slot = 64 * j + lane;
+            const bool valid = slot < n_slots;
+            const int sl = valid ? slot : 0;
+            XSlot xs;
+            const uint32_t *src = xlds + sl * kLdsSlotWords;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(src + 4 * q);
+                xs.p[4 * q] = v.x; xs.p[4 * q + 1] = v.y; xs.p[4 * q + 2] = v.z; xs.p[4 * q + 3] = v.w;
+            }
+            const f32x4v t = *reinterpret_cast<const f32x4v *>(src + 32);
+            xs.bias_lo = t[0];
+            xs.bias_hi = t[1];
+            xs.sx_lo = t[2];
+            xs.sx_hi = t[3];
+            const uint8_t *blk = rowp + (sl >> 2) * kBlockBytes;
+            const u32x4 h = *reinterpret_cast<const u32x4 *>(blk);
+            const u32x4 q0 = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * (sl & 3));
+            const u32x4 q1 = *reinterpret_cast<const u32x4 *>(blk + 32 + 32 * (sl & 3));
+            const float v = slot_dot(h, q0, q1, xs, scale_decode_for(sl & 3), magic);
+            acc += valid ? v : 0.0f;
+        }
+        const float total = lane_group_sum<64>(acc);
+        const uint32_t rres = EPI == kEpiAdd ? (uint32_t)__builtin_amdgcn_readlane((int)res, k) : 0u;
+        if (lane == 63) store_row<EPI>(rg, r0 + k, total, rres);
+    }
+}
+
 const DeviceInfo &device_info() {
     static thread_local int cached_dev = -1;
     static thread_local DeviceInfo info{0, 0};
@@ -787,8 +935,9 @@ static bool stream_fits(const GemvParams &p) {
     return true;
 }
 
-template <int LPR, int EPI>
-static hipError_t launch_stream(const GemvParams &p, int grid, hipStream_t st) {
+template <int LPR, int EPI, int G, int NBUF>
+static hipError_t launch_stream_g(const GemvParams &p, int grid, hipStream_t st) {
+    constexpr size_t lds = stream_lds<G, NBUF>();
     // the dynamic LDS limit, raised once per device (devices 0..63)
     static std::atomic<uint64_t> raised{0};
     int dev = 0;
@@ -796,23 +945,55 @@ static hipError_t launch_stream(const GemvParams &p, int grid, hipStream_t st) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(raised.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_stream_kernel<LPR, EPI, kStreamBufs>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStreamLds);
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_stream_kernel<LPR, EPI, G, NBUF>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         raised.fetch_or(bit, std::memory_order_acq_rel);
     }
-    gemv_stream_kernel<LPR, EPI, kStreamBufs><<<grid, 256, kStreamLds, st>>>(p);
+    gemv_stream_kernel<LPR, EPI, G, NBUF><<<grid, 256, lds, st>>>(p);
     return hipSuccess;
+}
+
+template <int EPI, int WB>
+static hipError_t launch_lds_stream_wb(const GemvParams &p, int grid, size_t x_lds, hipStream_t st) {
+    // the dynamic LDS limit (160 KB), raised once per device (devices 0..63)
+    static std::atomic<uint64_t> raised{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(raised.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_lds_stream_kernel<EPI, WB>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        raised.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    gemv_lds_stream_kernel<EPI, WB><<<grid, 256, (size_t)4 * WB + x_lds, st>>>(p);
+    return hipGetLastError();
+}
+
+// Wave buffers of 8 KB where a wave's rows fit them (two 4-wave workgroups
+// per CU then fit with x staged for K <= 11008), else 16 KB.
+template <int EPI>
+static hipError_t launch_lds_stream(const GemvParams &p, int grid, int64_t wave_bytes,
+                                    size_t x_lds, hipStream_t st) {
+    if (wave_bytes <= 8192) return launch_lds_stream_wb<EPI, 8192>(p, grid, x_lds, st);
+    return launch_lds_stream_wb<EPI, 16384>(p, grid, x_lds, st);
+}
+
+template <int LPR, int EPI>
+static hipError_t launch_stream(const GemvParams &p, int grid, int long_from, hipStream_t st) {
+    if (p.per_unit >= long_from)
+        return launch_stream_g<LPR, EPI, kStreamLongSteps, kStreamLongBufs>(p, grid, st);
+    return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamShortBufs>(p, grid, st);
 }
 
 template <int LPR, int EPI, int NT>
 static hipError_t launch_reg(const GemvParams &p, int grid, hipStream_t st) {
-    // RXQ4_GEMV_STREAM: 0 never, n > 0 from n steps per wave
-    const int min_steps = tuning().gemv_stream < 0   ? INT32_MAX
-                          : tuning().gemv_stream > 0 ? tuning().gemv_stream
-                                                     : kStreamMinSteps;
-    if (NT == 1 && p.per_unit >= min_steps && stream_fits(p))
-        return launch_stream<LPR, EPI>(p, grid, st);
+    // RXQ4_GEMV_STREAM: 0 the register kernel, n > 0 the long groups from n
+    // steps per wave (default kStreamMinSteps)
+    if (NT == 1 && tuning().gemv_stream >= 0 && stream_fits(p))
+        return launch_stream<LPR, EPI>(p, grid, tuning().gemv_stream > 0 ? tuning().gemv_stream : kStreamMinSteps, st);
     gemv_reg_kernel<LPR, EPI, kRegBatch, NT><<<grid, 256, 0, st>>>(p);
     return hipSuccess;
 }
@@ -840,12 +1021,25 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         }
         if (e != hipSuccess) return e;
     } else {
-        // LDS kernel: whole rows per wave, `waves_per_cu` waves per CU.
+        // LDS kernels: whole rows per wave, `waves_per_cu` waves per CU (8
+        // for the streamed kernel, 4 for the register-load kernel: down
+        // [2048 x 11008] in the decode chain of 36 layers, 633 against 660
+        // us per step streamed; 5.6 us for the register-load kernel at 4,
+        // which 8 waves per CU did not improve).
         const size_t lds = (size_t)NT * slots * kLdsSlotWords * sizeof(uint32_t);
         if (lds > 160 * 1024) return hipErrorInvalidValue;
-        const int64_t target = (int64_t)cus * (tuning().gemv_lds_waves_per_cu ? tuning().gemv_lds_waves_per_cu : 4);
-        int per_wave = (int)((p.total_rows + target - 1) / target);
-        if (per_wave < 1) per_wave = 1;
+        auto rows_per_wave = [&](int waves_per_cu) {
+            const int64_t target = (int64_t)cus * (tuning().gemv_lds_waves_per_cu ? tuning().gemv_lds_waves_per_cu : waves_per_cu);
+            return (int)std::max<int64_t>(1, (p.total_rows + target - 1) / target);
+        };
+        const int per_wave_s = rows_per_wave(8);
+        const int64_t wave_bytes = (int64_t)per_wave_s * p.nb * kBlockBytes;
+        if (NT == 1 && tuning().gemv_stream >= 0 && wave_bytes <= kLdsStreamWaveBytes &&
+            (size_t)4 * kLdsStreamWaveBytes + lds <= 160 * 1024 && stream_fits(p)) {
+            const int waves = assign_units(p, 1, per_wave_s);
+            return launch_lds_stream<EPI>(p, (waves + 3) / 4, wave_bytes, lds, st);
+        }
+        const int per_wave = rows_per_wave(4);
         const int waves = assign_units(p, 1, per_wave);
         const int grid = (waves + 3) / 4;
         if (lds > 64 * 1024) {

@@ -138,8 +138,8 @@ hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, 
 //   RXQ4_GEMM_NW=4|8 (the GEMM's waves per workgroup: 128- or 256-row tiles),
 //   RXQ4_TOKENS_WAVES=4|6|8 (waves of the LDS small-batch kernel's workgroups),
 //   RXQ4_TOKENS_LDS_SPLIT=n (its K split on long rows),
-//   RXQ4_GEMV_STREAM=0|n (one-token register GEMV: never streamed through
-//   LDS | streamed from n steps per wave; default 32).
+//   RXQ4_GEMV_STREAM=0|n (one-token register GEMV: 0 the register kernel,
+//   n the streamed kernel's long groups from n steps per wave, default 32).
 struct Tuning {
     int gemm_splits = 0;
     int gemv_waves_per_cu = 0;
@@ -153,7 +153,7 @@ struct Tuning {
     int tokens_waves = 0;
     int tokens_lds_split = 0;
     int gemm_nw = 0;  // 4 | 8: force the GEMM's four- or eight-wave workgroup
-    int gemv_stream = 0;  // -1 never, n > 0 from n steps per wave, 0 the default
+    int gemv_stream = 0;  // -1 register kernel, n > 0 long stream groups from n steps, 0 default
 };
 const Tuning &tuning();
 

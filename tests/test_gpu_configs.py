@@ -567,10 +567,13 @@ def digest(t):
 
 # (M, K): every register-kernel row length (K 256 .. 4096: 16 .. 1 rows a
 # step), one partial step, waves with a loop pass and a partial last group
-# (40000 x 1024: 10 steps a wave), and more rows than a buffer resource of
-# one wave's group
+# (40000 x 1024: 10 steps a wave), long waves (70001 x 2048: 35 steps), and
+# rows of more than 64 slots (the streamed LDS kernel, 8 waves per CU:
+# down's rows of 43 blocks, one a wave; 11- and 22-block rows, one a wave;
+# three rows a wave in 16 KB and 8 KB wave buffers)
 CASES = [(7, 256), (33, 512), (129, 1024), (2051, 2048), (301, 4096), (40000, 1024),
-         (70001, 2048)]
+         (70001, 2048), (2048, 11008), (100, 11008), (50, 2816), (1500, 5632),
+         (5000, 5632), (4100, 2816)]
 for M, K in CASES:
     print("streamed gemv", M, K, flush=True)
     Wn = util.weights(9500 + M, M, K)
@@ -608,23 +611,28 @@ print("stream ok", flush=True)
 """
 
 
-def test_gemv_streamed_kernel_forced():
-    """The one-token GEMV streamed through LDS (RXQ4_GEMV_STREAM=1: every
-    register-kernel launch; by default only waves of 32 steps or more, e.g.
-    the LM head) against the oracle, f32 / f16 / add (in place too), pair
-    and triple; RXQ4_GEMV_STREAM=0 runs the same cases on the register
-    kernel, and the two runs' outputs must be byte-identical (same
-    arithmetic)."""
+def test_gemv_streamed_kernel_configurations():
+    """The one-token GEMVs streamed through LDS against the oracle, f32 / f16
+    / add (in place too), pair and triple, in three launch configurations:
+    the default (register-kernel shapes: 1-step groups below 32 steps per
+    wave, 3-step groups from there, e.g. the LM head; longer rows: the
+    streamed LDS kernel where a wave's rows fit 16 KB), RXQ4_GEMV_STREAM=1
+    (3-step groups for every register-kernel launch) and RXQ4_GEMV_STREAM=0
+    (the register and LDS kernels); the three runs' outputs must be
+    byte-identical (same arithmetic)."""
     digests = {}
-    for mode in ("1", "0"):
-        env = dict(os.environ, RXQ4_GEMV_STREAM=mode)
+    for mode in ("", "1", "0"):
+        env = dict(os.environ)
+        env.pop("RXQ4_GEMV_STREAM", None)
+        if mode:
+            env["RXQ4_GEMV_STREAM"] = mode
         r = subprocess.run([sys.executable, "-c", STREAM_GEMV.replace("ROOT", repr(ROOT))],
                            env=env, capture_output=True, text=True, timeout=300)
         assert r.returncode == 0, mode + r.stdout[-1500:] + r.stderr[-3000:]
         assert "stream ok" in r.stdout
         digests[mode] = [l for l in r.stdout.splitlines() if l.startswith("DIGEST")]
-    assert len(digests["1"]) == 9
-    assert digests["1"] == digests["0"]
+    assert len(digests[""]) == 15
+    assert digests[""] == digests["1"] == digests["0"]
 
 
 KQ_FORCED_GEMM = r"""
