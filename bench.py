@@ -124,6 +124,8 @@ def host_cpu() -> dict:
 # every launch streams from HBM.
 LEGS = {
     "gate_up": (12, 2 * FFN, HIDDEN, 1, "pair"),
+    "qkv": (12, sum(QKV), HIDDEN, 1, "triple"),
+    "o": (12, HIDDEN, HIDDEN, 1, "add"),
     "down": (12, HIDDEN, FFN, 1, "add"),
     "lm_head": (12, VOCAB, HIDDEN, 1, "f32"),
     "embed": (12, VOCAB, HIDDEN, 4096, "embed"),
@@ -199,6 +201,12 @@ def run_leg(name: str, graph: bool = False) -> int:
             y = torch.empty(M, dtype=torch.float16, device=dev)
             res = gen(3, (M,), 1.0).half()
             run = lambda i: capi.gemv_add_f16(y, ws[i % n_copies], x, res, M, K, ggml_type=t)  # noqa: E731
+        elif kind == "triple":
+            y = torch.empty(M, dtype=torch.float16, device=dev)
+            a, b = QKV[0], QKV[0] + QKV[1]
+            run = lambda i: capi.gemv_multi_f16(  # noqa: E731
+                [(y[:a], ws[i % n_copies][:a], a, t), (y[a:b], ws[i % n_copies][a:b], b - a, t),
+                 (y[b:], ws[i % n_copies][b:], M - b, t)], x, K)
         else:
             y = torch.empty(M, dtype=torch.float16, device=dev)
             h = M // 2
@@ -461,7 +469,7 @@ def main() -> int:
     roofline = {"bound": "hbm", "achieved": round(gu_bytes / med / 1e3, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(gu_bytes / med / 1e3 / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "traffic_source": traffic_src,
-                "kernel": "gemv_reg_kernel<32,F16,2> (gate+up pair)",
+                "kernel": "gemv_stream_kernel<32,F16,1,3> (gate+up pair)",
                 "bytes_per_launch": gu_bytes, "us_per_launch": round(med, 3),
                 "us_mean": round(mean, 3),
                 "timing": "72 launches on distinct layers in a HIP graph, replayed 5 times between "
