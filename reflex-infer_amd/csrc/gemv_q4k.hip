@@ -785,9 +785,13 @@ __device__ __forceinline__ void wait_vmcnt_upto16(int n) {
 // that hold it, then reads its slots from LDS.  The residuals (kEpiAdd) of
 // the wave's rows are prefetched one per lane.
 constexpr int kLdsStreamWaveBytes = 16384;  // largest per-wave buffer
+// waves per workgroup: x is staged once per 8 waves (down, one row a wave,
+// one workgroup per CU: 5.50 us against 5.78-5.84 with two 4-wave
+// workgroups per CU; the decode chain 632 against 645 us)
+constexpr int kLdsStreamWaves = 8;
 
 template <int EPI, int WB>
-__global__ __launch_bounds__(256) void gemv_lds_stream_kernel(GemvParams p) {
+__global__ __launch_bounds__(64 * kLdsStreamWaves) void gemv_lds_stream_kernel(GemvParams p) {
     static_assert(WB % 1024 == 0 && WB <= kLdsStreamWaveBytes, "whole 1 KB loads, at most 16");
     constexpr int kLdsStreamLoads = WB / 1024;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -796,7 +800,7 @@ __global__ __launch_bounds__(256) void gemv_lds_stream_kernel(GemvParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wave = blockIdx.x * 4 + wv;
+    const int wave = blockIdx.x * kLdsStreamWaves + wv;
     const bool active = wave < p.total_units;
     const Range rg = range_of_unit(p, active ? wave : 0);
     const int r0 = active ? (wave - rg.first_unit) * p.per_unit : 0;
@@ -804,7 +808,7 @@ __global__ __launch_bounds__(256) void gemv_lds_stream_kernel(GemvParams p) {
     const int n_rows = r1 - r0;
     const uint32_t row_bytes = (uint32_t)p.nb * kBlockBytes;
     uint8_t *ring = smem + wv * WB;
-    uint32_t *xlds = reinterpret_cast<uint32_t *>(smem + 4 * WB);
+    uint32_t *xlds = reinterpret_cast<uint32_t *>(smem + kLdsStreamWaves * WB);
 
     // x, first round (slot tid), and the residuals of the wave's rows
     const int s_first = tid;
@@ -968,12 +972,17 @@ static hipError_t launch_lds_stream_wb(const GemvParams &p, int grid, size_t x_l
         if (e != hipSuccess) return e;
         raised.fetch_or(bit, std::memory_order_acq_rel);
     }
-    gemv_lds_stream_kernel<EPI, WB><<<grid, 256, (size_t)4 * WB + x_lds, st>>>(p);
+    gemv_lds_stream_kernel<EPI, WB><<<grid, 64 * kLdsStreamWaves, (size_t)kLdsStreamWaves * WB + x_lds,
+                                      st>>>(p);
     return hipGetLastError();
 }
 
-// Wave buffers of 8 KB where a wave's rows fit them (two 4-wave workgroups
-// per CU then fit with x staged for K <= 11008), else 16 KB.
+// Wave buffers of 8 KB where a wave's rows fit them, else 16 KB; `grid`
+// counts workgroups of kLdsStreamWaves waves.
+static size_t lds_stream_bytes(int64_t wave_bytes, size_t x_lds) {
+    return (size_t)kLdsStreamWaves * (wave_bytes <= 8192 ? 8192 : 16384) + x_lds;
+}
+
 template <int EPI>
 static hipError_t launch_lds_stream(const GemvParams &p, int grid, int64_t wave_bytes,
                                     size_t x_lds, hipStream_t st) {
@@ -1035,9 +1044,10 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         const int per_wave_s = rows_per_wave(8);
         const int64_t wave_bytes = (int64_t)per_wave_s * p.nb * kBlockBytes;
         if (NT == 1 && tuning().gemv_stream >= 0 && wave_bytes <= kLdsStreamWaveBytes &&
-            (size_t)4 * kLdsStreamWaveBytes + lds <= 160 * 1024 && stream_fits(p)) {
+            lds_stream_bytes(wave_bytes, lds) <= 160 * 1024 && stream_fits(p)) {
             const int waves = assign_units(p, 1, per_wave_s);
-            return launch_lds_stream<EPI>(p, (waves + 3) / 4, wave_bytes, lds, st);
+            return launch_lds_stream<EPI>(p, (waves + kLdsStreamWaves - 1) / kLdsStreamWaves,
+                                          wave_bytes, lds, st);
         }
         const int per_wave = rows_per_wave(4);
         const int waves = assign_units(p, 1, per_wave);
