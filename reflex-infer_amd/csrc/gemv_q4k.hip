@@ -476,7 +476,7 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-template <int LPR, int EPI, int G, int NBUF>
+template <int LPR, int EPI, int G, int NBUF, int NT>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     constexpr int RPS = 64 / LPR;
     constexpr int kStreamSteps = G;
@@ -484,8 +484,8 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     constexpr int kStreamLoads = StreamGeometry<G>::kLoads;
     constexpr int kStreamBufBytes = StreamGeometry<G>::kBufBytes;
     extern __shared__ __attribute__((aligned(16))) uint8_t ring[];
-    __shared__ __attribute__((aligned(16))) uint16_t xsh[kRegMaxK];
-    __shared__ float outs[4][kRegMaxRows];
+    __shared__ __attribute__((aligned(16))) uint16_t xsh[NT][kRegMaxK];
+    __shared__ float outs[NT][4][kRegMaxRows];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -502,12 +502,15 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     const int il = slot & 3;
     const int b = slot >> 2;
 
+    // x of NT tokens (token tk at x + tk * K) -> LDS, as the register kernel
     const int x_bytes = p.nb * kQK * 2;
-    const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(p.x, x_bytes);
+    const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(p.x, NT * x_bytes);
     constexpr int kXRounds = (RPS == 1) ? 2 : 1;
 #pragma unroll
-    for (int r = 0; r < kXRounds; ++r)
-        buffer_to_lds16(xrsrc, &xsh[(256 * r + 64 * wv) * 8], (256 * r + tid) * 16);
+    for (int tk = 0; tk < NT; ++tk)
+#pragma unroll
+        for (int r = 0; r < kXRounds; ++r)
+            buffer_to_lds16(xrsrc, &xsh[tk][(256 * r + 64 * wv) * 8], tk * x_bytes + (256 * r + tid) * 16);
     uint32_t res = 0;
     if (EPI == kEpiAdd) res = rg.res[min(row0 + lane, last)];
     __builtin_amdgcn_sched_barrier(0);
@@ -535,13 +538,14 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     wait_vmcnt<NBUF * kStreamLoads>();  // this wave's x copies (and residual) have landed
     lds_barrier();                      // ... and every other wave's
 
-    XSlot xs;
-    {
+    XSlot xs[NT];
+#pragma unroll
+    for (int tk = 0; tk < NT; ++tk) {
         u32x4 xraw[8];
-        const u32x4 *xs16 = reinterpret_cast<const u32x4 *>(xsh) + b * 32 + il * 8;
+        const u32x4 *xs16 = reinterpret_cast<const u32x4 *>(xsh[tk]) + b * 32 + il * 8;
 #pragma unroll
         for (int i = 0; i < 8; ++i) xraw[i] = xs16[i];
-        x_slot_from_raw(xraw, xs);
+        x_slot_from_raw(xraw, xs[tk]);
     }
     const ScaleDecode sd = scale_decode_for(il);
     const uint32_t magic = magic_vgpr();
@@ -565,8 +569,16 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
         for (int s = 0; s < kStreamSteps; ++s) {
             const int t = g * kStreamSteps + s;
             if (decltype(full)::value || t < n) {  // uniform
-                const float r = lane_group_sum<LPR>(slot_dot(h[s], q0[s], q1[s], xs, sd, magic));
-                if (slot == LPR - 1) outs[wv][t * RPS + sub] = r;
+                float v[NT];
+                if (NT == 1)
+                    v[0] = slot_dot(h[s], q0[s], q1[s], xs[0], sd, magic);
+                else
+                    slot_dot_nt<NT>(h[s], q0[s], q1[s], xs, sd, magic, v);
+#pragma unroll
+                for (int tk = 0; tk < NT; ++tk) {
+                    const float r = lane_group_sum<LPR>(v[tk]);
+                    if (slot == LPR - 1) outs[tk][wv][t * RPS + sub] = r;
+                }
             }
         }
     };
@@ -595,11 +607,15 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     });
 
     const int rows = min(n * RPS, rg.rows - row0);
-    if (lane < rows) store_row<EPI>(rg, row0 + lane, outs[wv][lane], res);
-    for (int r = 64; r < rows; r += 64) {
-        const int row = row0 + r + lane;
-        if (r + lane < rows)
-            store_row<EPI>(rg, row, outs[wv][r + lane], EPI == kEpiAdd ? rg.res[row] : 0u);
+#pragma unroll
+    for (int tk = 0; tk < NT; ++tk) {
+        const int64_t yoff = (int64_t)tk * p.y_stride;
+        if (lane < rows) store_row<EPI>(rg, row0 + lane, outs[tk][wv][lane], res, yoff);
+        for (int r = 64; r < rows; r += 64) {
+            const int row = row0 + r + lane;
+            if (r + lane < rows)
+                store_row<EPI>(rg, row, outs[tk][wv][r + lane], EPI == kEpiAdd ? rg.res[row] : 0u, yoff);
+        }
     }
 }
 
@@ -790,7 +806,7 @@ constexpr int kLdsStreamWaveBytes = 16384;  // largest per-wave buffer
 // workgroups per CU; the decode chain 632 against 645 us)
 constexpr int kLdsStreamWaves = 8;
 
-template <int EPI, int WB>
+template <int EPI, int WB, int NT>
 __global__ __launch_bounds__(64 * kLdsStreamWaves) void gemv_lds_stream_kernel(GemvParams p) {
     static_assert(WB % 1024 == 0 && WB <= kLdsStreamWaveBytes, "whole 1 KB loads, at most 16");
     constexpr int kLdsStreamLoads = WB / 1024;
@@ -810,11 +826,14 @@ __global__ __launch_bounds__(64 * kLdsStreamWaves) void gemv_lds_stream_kernel(G
     uint8_t *ring = smem + wv * WB;
     uint32_t *xlds = reinterpret_cast<uint32_t *>(smem + kLdsStreamWaves * WB);
 
-    // x, first round (slot tid), and the residuals of the wave's rows
+    // x, first round (slot tid of every token; token tk's slots follow
+    // token tk - 1's in LDS), and the residuals of the wave's rows
+    const int K = 256 * p.nb;
     const int s_first = tid;
     const int s_load = min(s_first, n_slots - 1);
-    u32x4 xraw[8];
-    load_x_raw(p.x, s_load >> 2, s_load & 3, xraw);
+    u32x4 xraw[NT][8];
+#pragma unroll
+    for (int tk = 0; tk < NT; ++tk) load_x_raw(p.x + (int64_t)tk * K, s_load >> 2, s_load & 3, xraw[tk]);
     uint32_t res = 0;
     if (EPI == kEpiAdd) res = rg.res[min(r0 + min(lane, max(n_rows - 1, 0)), rg.rows - 1)];
     __builtin_amdgcn_sched_barrier(0);
@@ -839,10 +858,16 @@ __global__ __launch_bounds__(64 * kLdsStreamWaves) void gemv_lds_stream_kernel(G
                 u32x4{xs.p[4 * k], xs.p[4 * k + 1], xs.p[4 * k + 2], xs.p[4 * k + 3]};
         *reinterpret_cast<f32x4v *>(dst + 32) = f32x4v{xs.bias_lo, xs.bias_hi, xs.sx_lo, xs.sx_hi};
     };
-    if (s_first < n_slots) stage(s_first, xraw);
+    if (s_first < n_slots) {
+#pragma unroll
+        for (int tk = 0; tk < NT; ++tk) stage(tk * n_slots + s_first, xraw[tk]);
+    }
     for (int s = s_first + blockDim.x; s < n_slots; s += blockDim.x) {
-        load_x_raw(p.x, s >> 2, s & 3, xraw);
-        stage(s, xraw);
+#pragma unroll
+        for (int tk = 0; tk < NT; ++tk) {
+            load_x_raw(p.x + (int64_t)tk * K, s >> 2, s & 3, xraw[0]);
+            stage(tk * n_slots + s, xraw[0]);
+        }
     }
     // the staged x is visible to every wave; no wait on the weight loads
     // here (__syncthreads would wait for them: its fence counts the loads
@@ -854,7 +879,9 @@ __global__ __launch_bounds__(64 * kLdsStreamWaves) void gemv_lds_stream_kernel(G
     const uint32_t magic = magic_vgpr();
     for (int k = 0; k < n_rows; ++k) {  // uniform
         const uint8_t *rowp = ring + k * row_bytes;
-        float acc = 0.0f;
+        float acc[NT];
+#pragma unroll
+        for (int tk = 0; tk < NT; ++tk) acc[tk] = 0.0f;
         for (int j = 0; j < J; ++j) {
             // item j of row k ends at byte k * row_bytes + min(64 (j+1), n_slots) / 4
             // blocks: the first `need` loads hold it
@@ -863,28 +890,40 @@ __global__ __launch_bounds__(64 * kLdsStreamWaves) void gemv_lds_stream_kernel(G
             const int slot = 64 * j + lane;
             const bool valid = slot < n_slots;
             const int sl = valid ? slot : 0;
-            XSlot xs;
-            const uint32_t *src = xlds + sl * kLdsSlotWords;
+            XSlot xs[NT];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const u32x4 v = *reinterpret_cast<const u32x4 *>(src + 4 * q);
-                xs.p[4 * q] = v.x; xs.p[4 * q + 1] = v.y; xs.p[4 * q + 2] = v.z; xs.p[4 * q + 3] = v.w;
+            for (int tk = 0; tk < NT; ++tk) {
+                const uint32_t *src = xlds + (tk * n_slots + sl) * kLdsSlotWords;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(src + 4 * q);
+                    xs[tk].p[4 * q] = v.x; xs[tk].p[4 * q + 1] = v.y;
+                    xs[tk].p[4 * q + 2] = v.z; xs[tk].p[4 * q + 3] = v.w;
+                }
+                const f32x4v t = *reinterpret_cast<const f32x4v *>(src + 32);
+                xs[tk].bias_lo = t[0];
+                xs[tk].bias_hi = t[1];
+                xs[tk].sx_lo = t[2];
+                xs[tk].sx_hi = t[3];
             }
-            const f32x4v t = *reinterpret_cast<const f32x4v *>(src + 32);
-            xs.bias_lo = t[0];
-            xs.bias_hi = t[1];
-            xs.sx_lo = t[2];
-            xs.sx_hi = t[3];
             const uint8_t *blk = rowp + (sl >> 2) * kBlockBytes;
             const u32x4 h = *reinterpret_cast<const u32x4 *>(blk);
             const u32x4 q0 = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * (sl & 3));
             const u32x4 q1 = *reinterpret_cast<const u32x4 *>(blk + 32 + 32 * (sl & 3));
-            const float v = slot_dot(h, q0, q1, xs, scale_decode_for(sl & 3), magic);
-            acc += valid ? v : 0.0f;
+            float v[NT];
+            if (NT == 1)
+                v[0] = slot_dot(h, q0, q1, xs[0], scale_decode_for(sl & 3), magic);
+            else
+                slot_dot_nt<NT>(h, q0, q1, xs, scale_decode_for(sl & 3), magic, v);
+#pragma unroll
+            for (int tk = 0; tk < NT; ++tk) acc[tk] += valid ? v[tk] : 0.0f;
         }
-        const float total = lane_group_sum<64>(acc);
         const uint32_t rres = EPI == kEpiAdd ? (uint32_t)__builtin_amdgcn_readlane((int)res, k) : 0u;
-        if (lane == 63) store_row<EPI>(rg, r0 + k, total, rres);
+#pragma unroll
+        for (int tk = 0; tk < NT; ++tk) {
+            const float total = lane_group_sum<64>(acc[tk]);
+            if (lane == 63) store_row<EPI>(rg, r0 + k, total, rres, (int64_t)tk * p.y_stride);
+        }
     }
 }
 
@@ -939,7 +978,7 @@ static bool stream_fits(const GemvParams &p) {
     return true;
 }
 
-template <int LPR, int EPI, int G, int NBUF>
+template <int LPR, int EPI, int G, int NBUF, int NT>
 static hipError_t launch_stream_g(const GemvParams &p, int grid, hipStream_t st) {
     constexpr size_t lds = stream_lds<G, NBUF>();
     // the dynamic LDS limit, raised once per device (devices 0..63)
@@ -949,16 +988,16 @@ static hipError_t launch_stream_g(const GemvParams &p, int grid, hipStream_t st)
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(raised.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_stream_kernel<LPR, EPI, G, NBUF>),
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_stream_kernel<LPR, EPI, G, NBUF, NT>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         raised.fetch_or(bit, std::memory_order_acq_rel);
     }
-    gemv_stream_kernel<LPR, EPI, G, NBUF><<<grid, 256, lds, st>>>(p);
+    gemv_stream_kernel<LPR, EPI, G, NBUF, NT><<<grid, 256, lds, st>>>(p);
     return hipSuccess;
 }
 
-template <int EPI, int WB>
+template <int EPI, int WB, int NT>
 static hipError_t launch_lds_stream_wb(const GemvParams &p, int grid, size_t x_lds, hipStream_t st) {
     // the dynamic LDS limit (160 KB), raised once per device (devices 0..63)
     static std::atomic<uint64_t> raised{0};
@@ -967,13 +1006,13 @@ static hipError_t launch_lds_stream_wb(const GemvParams &p, int grid, size_t x_l
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(raised.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_lds_stream_kernel<EPI, WB>),
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_lds_stream_kernel<EPI, WB, NT>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         raised.fetch_or(bit, std::memory_order_acq_rel);
     }
-    gemv_lds_stream_kernel<EPI, WB><<<grid, 64 * kLdsStreamWaves, (size_t)kLdsStreamWaves * WB + x_lds,
-                                      st>>>(p);
+    gemv_lds_stream_kernel<EPI, WB, NT><<<grid, 64 * kLdsStreamWaves, (size_t)kLdsStreamWaves * WB + x_lds,
+                                          st>>>(p);
     return hipGetLastError();
 }
 
@@ -983,26 +1022,28 @@ static size_t lds_stream_bytes(int64_t wave_bytes, size_t x_lds) {
     return (size_t)kLdsStreamWaves * (wave_bytes <= 8192 ? 8192 : 16384) + x_lds;
 }
 
-template <int EPI>
+template <int EPI, int NT>
 static hipError_t launch_lds_stream(const GemvParams &p, int grid, int64_t wave_bytes,
                                     size_t x_lds, hipStream_t st) {
-    if (wave_bytes <= 8192) return launch_lds_stream_wb<EPI, 8192>(p, grid, x_lds, st);
-    return launch_lds_stream_wb<EPI, 16384>(p, grid, x_lds, st);
+    if (wave_bytes <= 8192) return launch_lds_stream_wb<EPI, 8192, NT>(p, grid, x_lds, st);
+    return launch_lds_stream_wb<EPI, 16384, NT>(p, grid, x_lds, st);
 }
 
-template <int LPR, int EPI>
+template <int LPR, int EPI, int NT>
 static hipError_t launch_stream(const GemvParams &p, int grid, int long_from, hipStream_t st) {
     if (p.per_unit >= long_from)
-        return launch_stream_g<LPR, EPI, kStreamLongSteps, kStreamLongBufs>(p, grid, st);
-    return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamShortBufs>(p, grid, st);
+        return launch_stream_g<LPR, EPI, kStreamLongSteps, kStreamLongBufs, NT>(p, grid, st);
+    return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamShortBufs, NT>(p, grid, st);
 }
 
 template <int LPR, int EPI, int NT>
 static hipError_t launch_reg(const GemvParams &p, int grid, hipStream_t st) {
     // RXQ4_GEMV_STREAM: 0 the register kernel, n > 0 the long groups from n
     // steps per wave (default kStreamMinSteps)
-    if (NT == 1 && tuning().gemv_stream >= 0 && stream_fits(p))
-        return launch_stream<LPR, EPI>(p, grid, tuning().gemv_stream > 0 ? tuning().gemv_stream : kStreamMinSteps, st);
+    // one token and 2-4 tokens alike (gate+up [22016 x 2048] at 2 / 3
+    // tokens: 8.14 -> 7.87, 9.80 -> 9.49 us)
+    if (tuning().gemv_stream >= 0 && stream_fits(p))
+        return launch_stream<LPR, EPI, NT>(p, grid, tuning().gemv_stream > 0 ? tuning().gemv_stream : kStreamMinSteps, st);
     gemv_reg_kernel<LPR, EPI, kRegBatch, NT><<<grid, 256, 0, st>>>(p);
     return hipSuccess;
 }
@@ -1043,10 +1084,10 @@ static hipError_t launch_gemv_epi(GemvParams p, hipStream_t st) {
         };
         const int per_wave_s = rows_per_wave(8);
         const int64_t wave_bytes = (int64_t)per_wave_s * p.nb * kBlockBytes;
-        if (NT == 1 && tuning().gemv_stream >= 0 && wave_bytes <= kLdsStreamWaveBytes &&
+        if (tuning().gemv_stream >= 0 && wave_bytes <= kLdsStreamWaveBytes &&
             lds_stream_bytes(wave_bytes, lds) <= 160 * 1024 && stream_fits(p)) {
             const int waves = assign_units(p, 1, per_wave_s);
-            return launch_lds_stream<EPI>(p, (waves + kLdsStreamWaves - 1) / kLdsStreamWaves,
+            return launch_lds_stream<EPI, NT>(p, (waves + kLdsStreamWaves - 1) / kLdsStreamWaves,
                                           wave_bytes, lds, st);
         }
         const int per_wave = rows_per_wave(4);

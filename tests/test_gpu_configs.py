@@ -607,6 +607,22 @@ for Ms in ((11008, 3), (2048, 256, 256)):
     for y, w in zip(ys, Wn):
         assert util.rounded_ok(host16(y), orc.gemv_f32(w, K, x16)).all(), Ms
     print("DIGEST", Ms, *[digest(y) for y in ys], flush=True)
+# 2-4 tokens (RXQ4_MULTI_TOKEN_GEMV=1: the multi-token GEMV for every such
+# call): short and long waves, rows of 43 and 22 blocks
+for M, N, K in ((2051, 3, 2048), (70001, 2, 2048), (129, 2, 11008), (1500, 4, 5632),
+                (33, 4, 256)):
+    print("streamed multi-token", M, N, K, flush=True)
+    Wn = util.weights(9520 + M, M, K)
+    x16 = util.x_f16(9521 + N, (N, K))
+    ref32 = orc.gemm_tokens_f32(Wn, K, x16)
+    W, x = dev(Wn), dev(x16)
+    y16 = torch.empty((N, M), dtype=torch.float16, device="cuda")
+    capi.gemm_f16(y16, W, x, M, N, K)
+    y32 = torch.empty((N, M), dtype=torch.float32, device="cuda")
+    capi.gemm(y32, W, x.view(torch.float16), M, N, K)
+    assert util.rel_err(y32.cpu().numpy(), ref32) <= util.TOL, (M, N, K)
+    assert util.rounded_ok(host16(y16), ref32).all(), (M, N, K)
+    print("DIGEST", M, N, K, digest(y16), digest(y32), flush=True)
 print("stream ok", flush=True)
 """
 
@@ -618,11 +634,12 @@ def test_gemv_streamed_kernel_configurations():
     wave, 3-step groups from there, e.g. the LM head; longer rows: the
     streamed LDS kernel where a wave's rows fit 16 KB), RXQ4_GEMV_STREAM=1
     (3-step groups for every register-kernel launch) and RXQ4_GEMV_STREAM=0
-    (the register and LDS kernels); the three runs' outputs must be
-    byte-identical (same arithmetic)."""
+    (the register and LDS kernels); also 2-4 tokens on the multi-token
+    GEMV. The three runs' outputs must be byte-identical (same
+    arithmetic)."""
     digests = {}
     for mode in ("", "1", "0"):
-        env = dict(os.environ)
+        env = dict(os.environ, RXQ4_MULTI_TOKEN_GEMV="1")
         env.pop("RXQ4_GEMV_STREAM", None)
         if mode:
             env["RXQ4_GEMV_STREAM"] = mode
@@ -631,7 +648,7 @@ def test_gemv_streamed_kernel_configurations():
         assert r.returncode == 0, mode + r.stdout[-1500:] + r.stderr[-3000:]
         assert "stream ok" in r.stdout
         digests[mode] = [l for l in r.stdout.splitlines() if l.startswith("DIGEST")]
-    assert len(digests[""]) == 15
+    assert len(digests[""]) == 20
     assert digests[""] == digests["1"] == digests["0"]
 
 
