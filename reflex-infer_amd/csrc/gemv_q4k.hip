@@ -1124,15 +1124,15 @@ static hipError_t launch_multi_epi(GemvParams &p, int n_tok, hipStream_t st) {
     }
 }
 
-// 2 tokens: the multi-token GEMV.  3: it too when the rows give at least
-// one 64-row workgroup per CU (gate+up [22016 x 2048]: 10.2 against 11.4 us
-// on the MFMA small-batch kernel), else the MFMA kernel (down [2048 x
-// 11008] 9.0 against 9.3 us, QKV 4.4 against 5.0 us).  4: the MFMA kernel
-// (gate+up 11.3 against 11.6 us, down 9.1 against 11.1 us).  Graph replay,
-// distinct weights.
-bool gemv_multi_token_preferred(int n_tok, int M) {
-    const int cus = device_info().cu_count > 0 ? device_info().cu_count : 256;
-    return n_tok == 2 || (n_tok == 3 && (M + 63) / 64 >= cus);
+// 2 tokens: the multi-token GEMV.  3: it too for at least 4 MiB of weights
+// (streamed multi-token GEMV against the MFMA small-batch kernel: gate+up
+// [22016 x 2048] 9.4-9.8 against 10.8-10.9 us, down [2048 x 11008] 8.8
+// against 9.4-9.5, [5632 x 2048] 5.0 against 5.6), else the MFMA kernel
+// ([2560 x 2048] 4.55 against 4.21, [2048 x 2048] 4.12-4.18 against
+// 4.14-4.24).  4: the MFMA kernel (gate+up 11.2 against 10.5-10.6 us, down
+// 11.1 against 9.2-9.4).  Graph replay, distinct weights.
+bool gemv_multi_token_preferred(int n_tok, int M, int K) {
+    return n_tok == 2 || (n_tok == 3 && (int64_t)M * (K / 256) * kBlockBytes >= ((int64_t)4 << 20));
 }
 
 bool gemv_multi_token_fits(int n_tok, int K) {

@@ -76,9 +76,9 @@ hipError_t launch_gemv_multi_token(void *y, int y_dtype, const uint8_t *w, const
 // K/256 <= 16 blocks keep x in registers; longer rows stage every token's x
 // in LDS (n_tok * K/256 * 576 bytes, at most 160 KiB).
 bool gemv_multi_token_fits(int n_tok, int K);
-// Whether n_tok tokens on M rows run faster on the multi-token GEMV than on
-// the MFMA small-batch kernel (measured crossover).
-bool gemv_multi_token_preferred(int n_tok, int M);
+// Whether n_tok tokens on M rows of length K run faster on the multi-token
+// GEMV than on the MFMA small-batch kernel (measured crossover).
+bool gemv_multi_token_preferred(int n_tok, int M, int K);
 
 struct DeviceInfo {
     int cu_count;

@@ -224,7 +224,7 @@ int gemm_impl(const char *fn, void *y, int y_dtype, const void *w, int ggml_type
                               M, N, K, st, sc);
     else if (N <= rxq4::kMaxRegTokens && x_dtype == RXQ4_DTYPE_F16 &&
              (rxq4::tuning().multi_token_gemv > 0 ||
-              (rxq4::tuning().multi_token_gemv < 0 && rxq4::gemv_multi_token_preferred(N, M))) &&
+              (rxq4::tuning().multi_token_gemv < 0 && rxq4::gemv_multi_token_preferred(N, M, K))) &&
              rxq4::gemv_multi_token_fits(N, K))
         // 2 (or 3) fp16 tokens: the decode GEMV with every token's activations
         // in registers (one weight read, the nibble decode shared by the tokens)

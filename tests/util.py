@@ -95,14 +95,12 @@ def zipf_ids(seed: int, n: int, vocab: int, s: float = 1.1) -> np.ndarray:
 def gemv_path(N: int, M: int, K: int) -> bool:
     """Whether rxq4_gemm_f16 runs Q4_K with N fp16 tokens on the decode GEMV
     kernels (exact weights) rather than the MFMA kernels (fp16-rounded
-    weights): one token always; 2 tokens, and 3 when the rows give at least
-    one 64-row workgroup per CU, on the multi-token GEMV while its x fits
-    (registers up to 16 blocks a row, else N * K/256 * 576 bytes of LDS)."""
+    weights): one token always; 2 tokens, and 3 on at least 4 MiB of
+    weights, on the multi-token GEMV while its x fits (registers up to 16
+    blocks a row, else N * K/256 * 576 bytes of LDS)."""
     if N == 1:
         return True
-    import torch
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    if not (N == 2 or (N == 3 and -(-M // 64) >= cus)):
+    if not (N == 2 or (N == 3 and M * (K // 256) * 144 >= 4 << 20)):
         return False
     slots = 4 * (K // 256)
     return (slots <= 64 and 64 % slots == 0) or N * (K // 256) * 576 <= 160 * 1024
