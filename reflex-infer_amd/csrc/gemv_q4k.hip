@@ -448,12 +448,20 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 //   * shorter waves: 1-step groups x 3 buffers, QKV triple 3.36 -> 2.82,
 //     O add 3.19 -> 2.60, gate+up pair 6.85 -> 6.59 us (x 2 buffers: 2.79,
 //     2.57, 7.70; 1 x 4: 2.87, 2.71, 6.54; 3 x 2: gate+up 7.2; 6 or 8
-//     waves per CU slower on QKV).
+//     waves per CU slower on QKV);
+//   * of those, waves of 4 steps or more (gate+up: 11) issue the next
+//     group's LDS reads before this group's arithmetic, with 4 buffers:
+//     gate+up 6.55-6.86 -> 6.26-6.28 us; with 3 buffers 6.91-6.96; QKV (2
+//     steps) and O (1) ran slower with it (2.92 / 2.71-2.76).
 constexpr int kStepBytes = 64 * 36;
 // waves of at least this many steps take the long-group configuration
 constexpr int kStreamMinSteps = 32;
 constexpr int kStreamLongSteps = 3, kStreamLongBufs = 2;
 constexpr int kStreamShortSteps = 1, kStreamShortBufs = 3;
+// waves of kStreamMidSteps .. kStreamMinSteps-1 steps: 1-step groups x 4
+// buffers, the next group's LDS reads issued before this group's arithmetic
+constexpr int kStreamMidSteps = 4;
+constexpr int kStreamMidBufs = 4;
 
 template <int G>
 struct StreamGeometry {
@@ -476,7 +484,7 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-template <int LPR, int EPI, int G, int NBUF, int NT>
+template <int LPR, int EPI, int G, int NBUF, int NT, bool PF>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     constexpr int RPS = 64 / LPR;
     constexpr int kStreamSteps = G;
@@ -552,28 +560,31 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     // lane's slot in a step: block lane / 4 of the step, quant group lane & 3
     const int hdr_lds = (lane >> 2) * kBlockBytes;
     const int q_lds = hdr_lds + 16 + 32 * (lane & 3);
-    // One group: its 3 LDS reads per step all first (a lone wave on its SIMD
-    // would otherwise wait out the LDS latency per step), then the steps;
-    // `full` groups (all steps the wave's) skip the per-step test.
-    auto compute = [&](int g, int buf, auto full) __attribute__((always_inline)) {
-        const uint8_t *gb = my + buf * kStreamBufBytes;
+    // A group's LDS reads (3 per step), then its steps; `full` groups (all
+    // steps the wave's) skip the per-step test.
+    struct GroupRegs {
         u32x4 h[kStreamSteps], q0[kStreamSteps], q1[kStreamSteps];
+    };
+    auto read = [&](int buf, GroupRegs &R) __attribute__((always_inline)) {
+        const uint8_t *gb = my + buf * kStreamBufBytes;
 #pragma unroll
         for (int s = 0; s < kStreamSteps; ++s) {
             const uint8_t *sb = gb + s * kStepBytes;
-            h[s] = *reinterpret_cast<const u32x4 *>(sb + hdr_lds);
-            q0[s] = *reinterpret_cast<const u32x4 *>(sb + q_lds);
-            q1[s] = *reinterpret_cast<const u32x4 *>(sb + q_lds + 16);
+            R.h[s] = *reinterpret_cast<const u32x4 *>(sb + hdr_lds);
+            R.q0[s] = *reinterpret_cast<const u32x4 *>(sb + q_lds);
+            R.q1[s] = *reinterpret_cast<const u32x4 *>(sb + q_lds + 16);
         }
+    };
+    auto compute = [&](int g, const GroupRegs &R, auto full) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < kStreamSteps; ++s) {
             const int t = g * kStreamSteps + s;
             if (decltype(full)::value || t < n) {  // uniform
                 float v[NT];
                 if (NT == 1)
-                    v[0] = slot_dot(h[s], q0[s], q1[s], xs[0], sd, magic);
+                    v[0] = slot_dot(R.h[s], R.q0[s], R.q1[s], xs[0], sd, magic);
                 else
-                    slot_dot_nt<NT>(h[s], q0[s], q1[s], xs, sd, magic, v);
+                    slot_dot_nt<NT>(R.h[s], R.q0[s], R.q1[s], xs, sd, magic, v);
 #pragma unroll
                 for (int tk = 0; tk < NT; ++tk) {
                     const float r = lane_group_sum<LPR>(v[tk]);
@@ -585,26 +596,64 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvParams p) {
     using Full = std::integral_constant<bool, true>;
     using Tail = std::integral_constant<bool, false>;
 
-    // Steady state: groups g .. g+NBUF-1 in flight, group g+i in buffer i;
-    // each buffer is refilled once its group has been read (the reads'
-    // values are used before the refill is issued).  The tail computes the
-    // last NBUF groups with no loads behind them.
     int g = 0;
-    for (; g + NBUF < n_groups; g += NBUF) {
+    if constexpr (!PF) {
+        // Steady state: groups g .. g+NBUF-1 in flight, group g+i in buffer
+        // i; each buffer is refilled once its group has been read (the
+        // reads' values are used before the refill is issued).  The tail
+        // computes the last NBUF groups with no loads behind them.
+        for (; g + NBUF < n_groups; g += NBUF) {
+            static_for<0, NBUF>([&](auto i) __attribute__((always_inline)) {
+                constexpr int I = decltype(i)::value;
+                wait_vmcnt<(NBUF - 1) * kStreamLoads>();
+                GroupRegs R;
+                read(I, R);
+                compute(g + I, R, Full{});
+                __builtin_amdgcn_sched_barrier(0);
+                load(g + I + NBUF, I);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
         static_for<0, NBUF>([&](auto i) __attribute__((always_inline)) {
             constexpr int I = decltype(i)::value;
-            wait_vmcnt<(NBUF - 1) * kStreamLoads>();
-            compute(g + I, I, Full{});
-            __builtin_amdgcn_sched_barrier(0);
-            load(g + I + NBUF, I);
-            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<(NBUF - 1 - I) * kStreamLoads>();
+            GroupRegs R;
+            read(I, R);
+            compute(g + I, R, Tail{});
+        });
+    } else {
+        // The same, with the next group's LDS reads issued before this
+        // group's arithmetic (the LDS latency hides behind it): before
+        // group g+i is computed, group g+i+1 must have landed, so
+        // NBUF-2 groups are in flight during the arithmetic.
+        static_assert(NBUF >= 3, "a group in flight behind the prefetched one");
+        GroupRegs cur;
+        wait_vmcnt<(NBUF - 1) * kStreamLoads>();
+        read(0, cur);
+        for (; g + NBUF < n_groups; g += NBUF) {
+            static_for<0, NBUF>([&](auto i) __attribute__((always_inline)) {
+                constexpr int I = decltype(i)::value;
+                wait_vmcnt<(NBUF - 2) * kStreamLoads>();
+                GroupRegs nxt;
+                read((I + 1) % NBUF, nxt);
+                compute(g + I, cur, Full{});
+                __builtin_amdgcn_sched_barrier(0);
+                load(g + I + NBUF, I);
+                __builtin_amdgcn_sched_barrier(0);
+                cur = nxt;
+            });
+        }
+        static_for<0, NBUF>([&](auto i) __attribute__((always_inline)) {
+            constexpr int I = decltype(i)::value;
+            GroupRegs nxt;
+            if constexpr (I + 1 < NBUF) {
+                wait_vmcnt<(NBUF - 2 - I) * kStreamLoads>();
+                read(I + 1, nxt);
+            }
+            compute(g + I, cur, Tail{});
+            if constexpr (I + 1 < NBUF) cur = nxt;
         });
     }
-    static_for<0, NBUF>([&](auto i) __attribute__((always_inline)) {
-        constexpr int I = decltype(i)::value;
-        wait_vmcnt<(NBUF - 1 - I) * kStreamLoads>();
-        compute(g + I, I, Tail{});
-    });
 
     const int rows = min(n * RPS, rg.rows - row0);
 #pragma unroll
@@ -978,7 +1027,7 @@ static bool stream_fits(const GemvParams &p) {
     return true;
 }
 
-template <int LPR, int EPI, int G, int NBUF, int NT>
+template <int LPR, int EPI, int G, int NBUF, int NT, bool PF>
 static hipError_t launch_stream_g(const GemvParams &p, int grid, hipStream_t st) {
     constexpr size_t lds = stream_lds<G, NBUF>();
     // the dynamic LDS limit, raised once per device (devices 0..63)
@@ -988,12 +1037,12 @@ static hipError_t launch_stream_g(const GemvParams &p, int grid, hipStream_t st)
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(raised.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_stream_kernel<LPR, EPI, G, NBUF, NT>),
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_stream_kernel<LPR, EPI, G, NBUF, NT, PF>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         raised.fetch_or(bit, std::memory_order_acq_rel);
     }
-    gemv_stream_kernel<LPR, EPI, G, NBUF, NT><<<grid, 256, lds, st>>>(p);
+    gemv_stream_kernel<LPR, EPI, G, NBUF, NT, PF><<<grid, 256, lds, st>>>(p);
     return hipSuccess;
 }
 
@@ -1032,8 +1081,10 @@ static hipError_t launch_lds_stream(const GemvParams &p, int grid, int64_t wave_
 template <int LPR, int EPI, int NT>
 static hipError_t launch_stream(const GemvParams &p, int grid, int long_from, hipStream_t st) {
     if (p.per_unit >= long_from)
-        return launch_stream_g<LPR, EPI, kStreamLongSteps, kStreamLongBufs, NT>(p, grid, st);
-    return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamShortBufs, NT>(p, grid, st);
+        return launch_stream_g<LPR, EPI, kStreamLongSteps, kStreamLongBufs, NT, false>(p, grid, st);
+    if (p.per_unit >= kStreamMidSteps)
+        return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamMidBufs, NT, true>(p, grid, st);
+    return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamShortBufs, NT, false>(p, grid, st);
 }
 
 template <int LPR, int EPI, int NT>
