@@ -464,10 +464,89 @@ __device__ __forceinline__ void kq_multi_unit(const KqMultiParams &p, const KqMu
     }
 }
 
+// The units of wave u0 and its successors u0 + n_waves, ...; each unit's
+// type is dispatched.
+__device__ __forceinline__ void kq_multi_units(const KqMultiParams &p, int u0, int lane,
+                                               const XLds &xl) {
+    const int n_waves = gridDim.x * 4;
+    for (int u = u0; u < p.n_units; u += n_waves) {
+        const int ri = (p.n_ranges > 1 && u >= p.r[1].unit0) + (p.n_ranges > 2 && u >= p.r[2].unit0);
+        const KqMultiRange &r = p.r[ri];
+        const int lu = u - r.unit0;
+        switch (r.type) {
+            case 12: kq_multi_unit<12>(p, r, lu, lane, xl); break;
+            case 13: kq_multi_unit<13>(p, r, lu, lane, xl); break;
+            default: kq_multi_unit<14>(p, r, lu, lane, xl); break;
+        }
+    }
+}
+
+// Packed rows, K <= 4096 (one x run of 16 per thread): the wave's first
+// unit (type T) loads its weights right behind the thread's x run, x is
+// staged and a barrier that waits for LDS only follows, so the weights stay
+// in flight across the staging (loads complete in order: x first).  The
+// unit's arithmetic and the staged x are those of kq_multi_unit.
+template <int T>
+__device__ __forceinline__ void kq_multi_first_packed(const KqMultiParams &p, int u0, int uc,
+                                                      int ri, int tid, int lane, u32x4 *xs,
+                                                      float *sums, const XLds &xl) {
+    constexpr int BYTES = KqFormat<T>::kBytes;
+    const int n_runs = p.K >> 4;
+    const int rx = min(tid, n_runs - 1);
+    const u32x4 *xg = reinterpret_cast<const u32x4 *>(p.x);
+    const u32x4 xa = xg[2 * rx], xb = xg[2 * rx + 1];
+    __builtin_amdgcn_sched_barrier(0);
+    const KqMultiRange &r = p.r[ri];
+    const int lu = uc - r.unit0;
+    const int sub = lane / p.slots, slot = lane - sub * p.slots;
+    const int r0 = lu * p.rows_per;
+    const int n = min(p.rows_per, r.M - r0);
+    const RowRes rr = row_rsrc(r.w + (int64_t)r0 * r.row_bytes, n * r.row_bytes);
+    const int b = slot >> 2, u = slot & 3;
+    const int boff = rr.ex + sub * r.row_bytes + b * BYTES;
+    Slot<T> S;
+    S.load(rr.rs, boff, u);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < n_runs) {
+        xs[2 * tid] = xa;
+        xs[2 * tid + 1] = xb;
+        const uint32_t w8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        float sx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            sx += f16_bits_to_f32(w8[i] & 0xFFFFu);
+            sx += f16_bits_to_f32(w8[i] >> 16);
+        }
+        sums[tid] = sx;
+    }
+    wait_lgkmcnt0();
+    lds_barrier();
+    if (u0 < p.n_units) {
+        float v = S.dot(boff, u, b * 256, xl);
+        for (int o = p.slots >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (slot == 0 && sub < n) r.y[r0 + sub] = f32_to_f16_bits(v);
+    }
+    kq_multi_units(p, u0 + gridDim.x * 4, lane, xl);
+}
+
 __global__ __launch_bounds__(256) void kq_multi_kernel(KqMultiParams p) {
     extern __shared__ u32x4 kq_smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
+    const int u0 = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (p.rows_per > 0 && (p.K >> 4) <= 256) {
+        u32x4 *xs = kq_smem;
+        float *sums = reinterpret_cast<float *>(kq_smem + (p.K >> 3));
+        const XLds xl{kq_smem, sums};
+        const int uc = min(u0, p.n_units - 1);
+        const int ri = (p.n_ranges > 1 && uc >= p.r[1].unit0) + (p.n_ranges > 2 && uc >= p.r[2].unit0);
+        switch (p.r[ri].type) {
+            case 12: kq_multi_first_packed<12>(p, u0, uc, ri, tid, lane, xs, sums, xl); break;
+            case 13: kq_multi_first_packed<13>(p, u0, uc, ri, tid, lane, xs, sums, xl); break;
+            default: kq_multi_first_packed<14>(p, u0, uc, ri, tid, lane, xs, sums, xl); break;
+        }
+        return;
+    }
     {
         u32x4 *xs = kq_smem;
         float *sums = reinterpret_cast<float *>(kq_smem + (p.K >> 3));
@@ -488,18 +567,7 @@ __global__ __launch_bounds__(256) void kq_multi_kernel(KqMultiParams p) {
     }
     __syncthreads();
     const XLds xl{kq_smem, reinterpret_cast<const float *>(kq_smem + (p.K >> 3))};
-    const int n_waves = gridDim.x * 4;
-    for (int u = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(tid >> 6); u < p.n_units;
-         u += n_waves) {
-        const int ri = (p.n_ranges > 1 && u >= p.r[1].unit0) + (p.n_ranges > 2 && u >= p.r[2].unit0);
-        const KqMultiRange &r = p.r[ri];
-        const int lu = u - r.unit0;
-        switch (r.type) {
-            case 12: kq_multi_unit<12>(p, r, lu, lane, xl); break;
-            case 13: kq_multi_unit<13>(p, r, lu, lane, xl); break;
-            default: kq_multi_unit<14>(p, r, lu, lane, xl); break;
-        }
-    }
+    kq_multi_units(p, u0, lane, xl);
 }
 
 template <int T, int EPI, bool PACKED>
