@@ -444,7 +444,12 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 //     2 x 4 or 4 x 2 (18 KB in flight) 31.0-31.4, 2 x 2 31.4-32.0, 1-step
 //     groups 32.0-33.0; without the nontemporal bit 35.2-35.5; with 8 waves
 //     per CU 31.2-31.4; groups dealt round-robin over the range's waves
-//     (rows stored per step) 35.6-37.2;
+//     (rows stored per step) 35.6-37.2.  With the next group's LDS reads
+//     issued before this group's arithmetic (below), 1-step groups x 5
+//     buffers against 3 x 2: LM head 30.1-30.2 -> 28.9-29.8, [151936 x
+//     1024] 16.9 -> 16.5-16.6, [65536 x 2048] 14.8 -> 14.4, [100000 x 2048]
+//     add 21.2-21.4 -> 20.7-20.8 us (1 x 4 / 1 x 6 / 2 x 4 / 2 x 5: LM head
+//     30.1 / 29.4-29.8 / 30.3-30.6 / 30.6-30.9);
 //   * shorter waves: 1-step groups x 3 buffers, QKV triple 3.36 -> 2.82,
 //     O add 3.19 -> 2.60, gate+up pair 6.85 -> 6.59 us (x 2 buffers: 2.79,
 //     2.57, 7.70; 1 x 4: 2.87, 2.71, 6.54; 3 x 2: gate+up 7.2; 6 or 8
@@ -456,7 +461,7 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvParams p) {
 constexpr int kStepBytes = 64 * 36;
 // waves of at least this many steps take the long-group configuration
 constexpr int kStreamMinSteps = 32;
-constexpr int kStreamLongSteps = 3, kStreamLongBufs = 2;
+constexpr int kStreamLongSteps = 1, kStreamLongBufs = 5;
 constexpr int kStreamShortSteps = 1, kStreamShortBufs = 3;
 // waves of kStreamMidSteps .. kStreamMinSteps-1 steps: 1-step groups x 4
 // buffers, the next group's LDS reads issued before this group's arithmetic
@@ -1081,7 +1086,7 @@ static hipError_t launch_lds_stream(const GemvParams &p, int grid, int64_t wave_
 template <int LPR, int EPI, int NT>
 static hipError_t launch_stream(const GemvParams &p, int grid, int long_from, hipStream_t st) {
     if (p.per_unit >= long_from)
-        return launch_stream_g<LPR, EPI, kStreamLongSteps, kStreamLongBufs, NT, false>(p, grid, st);
+        return launch_stream_g<LPR, EPI, kStreamLongSteps, kStreamLongBufs, NT, true>(p, grid, st);
     if (p.per_unit >= kStreamMidSteps)
         return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamMidBufs, NT, true>(p, grid, st);
     return launch_stream_g<LPR, EPI, kStreamShortSteps, kStreamShortBufs, NT, false>(p, grid, st);
@@ -1089,7 +1094,7 @@ static hipError_t launch_stream(const GemvParams &p, int grid, int long_from, hi
 
 template <int LPR, int EPI, int NT>
 static hipError_t launch_reg(const GemvParams &p, int grid, hipStream_t st) {
-    // RXQ4_GEMV_STREAM: 0 the register kernel, n > 0 the long groups from n
+    // RXQ4_GEMV_STREAM: 0 the register kernel, n > 0 the long-wave configuration from n
     // steps per wave (default kStreamMinSteps)
     // one token and 2-4 tokens alike (gate+up [22016 x 2048] at 2 / 3
     // tokens: 8.14 -> 7.87, 9.80 -> 9.49 us)

@@ -630,10 +630,11 @@ print("stream ok", flush=True)
 def test_gemv_streamed_kernel_configurations():
     """The one-token GEMVs streamed through LDS against the oracle, f32 / f16
     / add (in place too), pair and triple, in three launch configurations:
-    the default (register-kernel shapes: 1-step groups below 32 steps per
-    wave, 3-step groups from there, e.g. the LM head; longer rows: the
-    streamed LDS kernel where a wave's rows fit 16 KB), RXQ4_GEMV_STREAM=1
-    (3-step groups for every register-kernel launch) and RXQ4_GEMV_STREAM=0
+    the default (register-kernel shapes: 3 buffers below 4 steps per wave,
+    4 with the next group's LDS reads issued early below 32, 5 from there,
+    e.g. the LM head; longer rows: the streamed LDS kernel where a wave's
+    rows fit 16 KB), RXQ4_GEMV_STREAM=1 (the 5-buffer configuration for
+    every register-kernel launch) and RXQ4_GEMV_STREAM=0
     (the register and LDS kernels); also 2-4 tokens on the multi-token
     GEMV. The three runs' outputs must be byte-identical (same
     arithmetic)."""
