@@ -428,9 +428,10 @@ def main() -> int:
     # ------------------------------------------------ per-kernel durations
     def per_launch(launch, n, reps=5):
         """Duration of one `launch(i)` as the decode graph issues it: n
-        launches (distinct weights) captured in a HIP graph on `stream` and
-        replayed `reps` times between events recorded on `stream`; returns
-        the median and mean over the replays of elapsed / n, in us."""
+        launches (distinct weights) captured in a HIP graph on `stream`,
+        replayed 10 times untimed (the clock ramps over the first replays)
+        and `reps` times between events recorded on `stream`; returns the
+        median and mean over the timed replays of elapsed / n, in us."""
         with torch.cuda.stream(stream):
             for i in range(3):
                 launch(i)
@@ -440,7 +441,8 @@ def main() -> int:
             for i in range(n):
                 launch(i)
         with torch.cuda.stream(stream):
-            g.replay()
+            for _ in range(10):
+                g.replay()
         torch.cuda.synchronize()
         d = []
         for _ in range(reps):
