@@ -51,8 +51,9 @@ Profiling entry points (no timing, for rocprofv3 counter passes):
                     shapes, small batch gate_up_m8 / gate_up_m16 / down_m16,
                     attn_prefill)
   --leg NAME --graph  the same workload as 72 launches in a HIP graph,
-                    replayed 10 times; prints the per-launch time from HIP
-                    events (the figure the kernel trace is compared with)
+                    replayed 20 times untimed and 10 times timed; prints the
+                    per-launch time from HIP events (the figure the kernel
+                    trace is compared with)
   --calibrate-copy  a 256 MiB device copy, to scale FETCH_SIZE / WRITE_SIZE
 """
 from __future__ import annotations
@@ -166,16 +167,14 @@ def run_leg(name: str, graph: bool = False) -> int:
                   for i in range(n_copies)]
         qp = gen(73_000, (m, AH * AD), 1.0).half()
         op = torch.empty_like(qp)
-        torch.cuda.synchronize()
-        for i in range(launches):
-            k, v = caches[i % n_copies]
-            capi.attention_prefill_f16(op, qp, k, v, AH, AKV, AD, m, 0, AD ** -0.5)
-        torch.cuda.synchronize()
-        print(json.dumps({"leg": name, "launches": launches, "kv_copies": n_copies}), flush=True)
-        return 0
-    n_copies = 3 if M == VOCAB else max(2, -(-(600 << 20) // qbytes(M, K)))
-    ws = [capi.quantize_ggml(gen(80_000 + i, (M, K), 0.02), t) for i in range(n_copies)]
-    if kind == "embed":
+        run = lambda i: capi.attention_prefill_f16(  # noqa: E731
+            op, qp, caches[i % n_copies][0], caches[i % n_copies][1], AH, AKV, AD, m, 0, AD ** -0.5)
+    else:
+        n_copies = 3 if M == VOCAB else max(2, -(-(600 << 20) // qbytes(M, K)))
+        ws = [capi.quantize_ggml(gen(80_000 + i, (M, K), 0.02), t) for i in range(n_copies)]
+    if kind == "attn_prefill":
+        pass
+    elif kind == "embed":
         rng = np.random.default_rng(5)
         ranks = np.arange(1, VOCAB + 1, dtype=np.float64)
         cdf = np.cumsum(ranks ** -1.1)

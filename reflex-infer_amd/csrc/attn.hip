@@ -662,8 +662,8 @@ __global__ __launch_bounds__(256 * G, 2 / G) void attn_prefill_mfma(AttnParams p
         for (int st = 0; st < 4; ++st)
 #pragma unroll
             for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[st][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = max_xor_rows<16>(mx);
+        mx = max_xor_rows<32>(mx);
         const float m_new = fmaxf(m, mx);
         const bool live = m_new != -INFINITY;  // something visible so far
         const float corr = live ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
@@ -697,8 +697,8 @@ __global__ __launch_bounds__(256 * G, 2 / G) void attn_prefill_mfma(AttnParams p
                 ph[st >> 1][2 * (st & 1) + (i >> 1)] = hi;
                 pl[st >> 1][2 * (st & 1) + (i >> 1)] = lo;
             }
-        sum += __shfl_xor(sum, 16, 64);
-        sum += __shfl_xor(sum, 32, 64);
+        sum = sum_xor_rows<16>(sum);
+        sum = sum_xor_rows<32>(sum);
         l = l * corr + sum;
         m = m_new;
         // O^T = corr * O^T + V^T . P^T
@@ -906,8 +906,8 @@ __global__ __launch_bounds__(256, 2) void attn_decode_mfma(AttnParams p) {
                 sv[i] = p0 + 16 * w + 4 * g + i < end ? s : -INFINITY;
             }
             float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = max_xor_rows<16>(mx);
+            mx = max_xor_rows<32>(mx);
             const float m_new = fmaxf(m, mx);
             const bool live = m_new != -INFINITY;
             const float corr = live ? __builtin_amdgcn_exp2f(m - m_new) : 1.0f;
@@ -919,8 +919,8 @@ __global__ __launch_bounds__(256, 2) void attn_decode_mfma(AttnParams p) {
                 sum += e[i];
                 if (I8) e[i] *= vsc[b][i];
             }
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
+            sum = sum_xor_rows<16>(sum);
+            sum = sum_xor_rows<32>(sum);
             l = l * corr + sum;
             m = m_new;
             // P^T hi / lo (lo = RNE_f16(e - f32(hi)), exact difference, one rounding)

@@ -98,6 +98,44 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Combine each lane's x with x of lane ^ 16 (ROW = 16) or lane ^ 32 (ROW =
+// 32) on the VALU: v_permlane{16,32}_swap on two copies of x leaves, in
+// every lane, its own value in one result and its partner's in the other
+// (which one depends on the lane), so max / sum of the two results equal
+// fmaxf / + of x and the partner's x (both commutative) with no LDS
+// instruction (__shfl_xor is a ds_bpermute, queued behind LDS traffic).
+template <int ROW>
+__device__ __forceinline__ void swap_rows(float x, float &a, float &b) {
+    static_assert(ROW == 16 || ROW == 32, "row swaps of 16 or 32 lanes");
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    uint32_t r0, r1;
+    if constexpr (ROW == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        r0 = r[0];
+        r1 = r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        r0 = r[0];
+        r1 = r[1];
+    }
+    a = __builtin_bit_cast(float, r0);
+    b = __builtin_bit_cast(float, r1);
+}
+
+template <int ROW>
+__device__ __forceinline__ float max_xor_rows(float x) {
+    float a, b;
+    swap_rows<ROW>(x, a, b);
+    return fmaxf(a, b);
+}
+
+template <int ROW>
+__device__ __forceinline__ float sum_xor_rows(float x) {
+    float a, b;
+    swap_rows<ROW>(x, a, b);
+    return a + b;
+}
+
 // Workgroup barrier without the fence of __syncthreads (which waits for all
 // outstanding vector memory operations); callers wait for what they need.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
