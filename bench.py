@@ -565,7 +565,7 @@ def main() -> int:
 
         def lm_launch(i):
             capi.gemv_f32(logits, heads[i % 3], x_h, VOCAB, HIDDEN, stream=sp)
-        med, _ = per_launch(lm_launch, 20)
+        med, _ = per_launch(lm_launch, 72)
         b = qbytes(VOCAB, HIDDEN) + 2 * HIDDEN + 4 * VOCAB
         kernels["lm_head_f32_151936x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
 
@@ -581,7 +581,7 @@ def main() -> int:
 
         def emb_launch(i):
             capi.embed_rows_f16(emb, heads[i % 3], VOCAB, ids, HIDDEN, stream=sp)
-        med, _ = per_launch(emb_launch, 20)
+        med, _ = per_launch(emb_launch, 72)
         uniq = int(np.unique(ids_np).size)
         table_host = heads[0].cpu().numpy() if not args.no_cpu_baseline else None
         b = uniq * qbytes(1, HIDDEN) + 4096 * HIDDEN * 2 + 4096 * 4
@@ -600,13 +600,13 @@ def main() -> int:
 
         def lm6_launch(i):
             capi.gemv_f32(logits, heads6[i % 3], x_h, VOCAB, HIDDEN, stream=sp, ggml_type=14)
-        med, _ = per_launch(lm6_launch, 21)
+        med, _ = per_launch(lm6_launch, 72)
         b = q6b(VOCAB, HIDDEN) + 2 * HIDDEN + 4 * VOCAB
         kernels["q6k_lm_head_f32_151936x2048"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
 
         def emb6_launch(i):
             capi.embed_rows_f16(emb, heads6[i % 3], VOCAB, ids, HIDDEN, stream=sp, ggml_type=14)
-        med, _ = per_launch(emb6_launch, 21)
+        med, _ = per_launch(emb6_launch, 72)
         b = uniq * q6b(1, HIDDEN) + 4096 * HIDDEN * 2 + 4096 * 4
         kernels["q6k_embed_gather_4096_zipf"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
         del heads6
@@ -653,7 +653,7 @@ def main() -> int:
         def prefill_launch(i):
             k, v = caches[i % 36]
             capi.attention_prefill_f16(op, qp, k, v, AH, AKV, AD, 512, 0, AD ** -0.5, stream=sp)
-        med, _ = per_launch(prefill_launch, 8)
+        med, _ = per_launch(prefill_launch, 72)
         fl = 4.0 * AH * AD * sum(t + 1 for t in range(512))
         kernels["attn_prefill_fp16_512"] = {"us": round(med, 3), "TFLOPs": round(fl / med / 1e6, 2)}
         del caches
@@ -672,7 +672,7 @@ def main() -> int:
                 k, v = vkv[i % 8]
                 torch.nn.functional.scaled_dot_product_attention(vq[i % 8], k, v, is_causal=True)
             with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
-                med, _ = per_launch(sdpa_launch, 8)
+                med, _ = per_launch(sdpa_launch, 72)
             extras["vendor_sdpa_prefill_512"] = {"us": round(med, 3), "TFLOPs": round(fl / med / 1e6, 2)}
             del vq, vkv
         except Exception as ex:  # no flash backend on this build: report, do not fall back
@@ -684,7 +684,7 @@ def main() -> int:
         def attn_long(i):
             k, v = long_kv[i % 9]
             capi.attention_decode_f16(oa, qa, k, v, AH, AKV, AD, 16384, AD ** -0.5, stream=sp)
-        med, _ = per_launch(attn_long, 36)
+        med, _ = per_launch(attn_long, 72)
         b = 2 * 16384 * AKV * AD * 2
         kernels["attn_decode_fp16_16384"] = {"us": round(med, 3), "GBps": round(b / med / 1e3, 1)}
         del long_kv
