@@ -397,16 +397,30 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     if (wv == 0) {
         const bool ok = lane < p.n_chunks;
         if (!ok) m = -INFINITY;
-        float M = m;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        // max over the 64 lanes (exact in any order): row swaps, then DPP
+        // rotations within 16-lane rows (no LDS instruction)
+        float M = max_xor_rows<32>(m);
+        M = max_xor_rows<16>(M);
+        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x128, 0xF, 0xF, false)));
+        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x124, 0xF, 0xF, false)));
+        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x122, 0xF, 0xF, false)));
+        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x121, 0xF, 0xF, false)));
         const float e = ok ? expf(m - M) : 0.0f;
         wgt[lane] = e;
         // Butterfly sum: a fixed association (every lane gets the same
-        // value), so the result does not depend on scheduling.
+        // value), so the result does not depend on scheduling.  Partners
+        // lane ^ 1, ^ 2, ^ 4, ^ 8, ^ 16, ^ 32 in that order, on the VALU:
+        // quad permutations, then the half-row mirror and row_ror:8 (after
+        // the smaller steps they reach lanes holding the partner's value),
+        // then the row swaps; each step adds the same two values in the same
+        // order as a shuffle butterfly would.
         float L = ok ? e * l : 0.0f;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) L += __shfl_xor(L, o, 64);
+        L = dpp_row_add<0xB1>(L);   // quad_perm [1,0,3,2]
+        L = dpp_row_add<0x4E>(L);   // quad_perm [2,3,0,1]
+        L = dpp_row_add<0x141>(L);  // row_half_mirror
+        L = dpp_row_add<0x128>(L);  // row_ror:8
+        L = sum_xor_rows<16>(L);
+        L = sum_xor_rows<32>(L);
         if (lane == 0) inv_l = L > 0.0f ? 1.0f / L : 0.0f;
     }
     lds_sync();

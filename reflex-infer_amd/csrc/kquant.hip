@@ -109,6 +109,16 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 // x in LDS: fp16 [K] followed by fp32 sums of each 16-element run [K/16].
+// Sum over aligned groups of `slots` lanes (uniform; a power of two, at most
+// 64): the __shfl_xor butterfly, on the VALU (butterfly_sum, bit-identical)
+// for groups of 32 and 64.
+__device__ __forceinline__ float kq_row_sum(float v, int slots) {
+    if (slots == 64) return butterfly_sum<64>(v);
+    if (slots == 32) return butterfly_sum<32>(v);
+    for (int q = slots >> 1; q > 0; q >>= 1) v += __shfl_xor(v, q, 64);
+    return v;
+}
+
 struct XLds {
     const u32x4 *x;   // 8 fp16 per element
     const float *sum;
@@ -366,7 +376,7 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
         };
         auto finish = [&](const Step &o) {
             float v = o.s.dot(o.r.ex + boff, u, b * 256, xl);
-            for (int q = p.slots >> 1; q > 0; q >>= 1) v += __shfl_xor(v, q, 64);
+            v = kq_row_sum(v, p.slots);
             if (slot == 0 && sub < o.n) kq_store<EPI>(p, o.r0 + sub, v, o.res);
         };
         stage_x();
@@ -404,8 +414,7 @@ __global__ __launch_bounds__(256) void kq_gemv_kernel(KqGemvParams p) {
                 v += A.dot(o0, s0 & 3, min(b0, p.nb - 1) * 256, xl);
                 if (c + 1 < n_iter) v += B.dot(o1, s1 & 3, min(b1, p.nb - 1) * 256, xl);
             }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            v = butterfly_sum<64>(v);
             if (lane == 0) kq_store<EPI>(p, row, v, res);
         }
     }
@@ -442,7 +451,7 @@ __device__ __forceinline__ void kq_multi_unit(const KqMultiParams &p, const KqMu
         Slot<T> S;
         S.load(rr.rs, boff, u);
         float v = S.dot(boff, u, b * 256, xl);
-        for (int o = p.slots >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        v = kq_row_sum(v, p.slots);
         if (slot == 0 && sub < n) r.y[r0 + sub] = f32_to_f16_bits(v);
     } else {
         const RowRes rr = row_rsrc(r.w + (int64_t)lu * r.row_bytes, r.row_bytes);
@@ -458,8 +467,7 @@ __device__ __forceinline__ void kq_multi_unit(const KqMultiParams &p, const KqMu
             v += A.dot(o0, s0 & 3, min(b0, p.nb - 1) * 256, xl);
             if (c + 1 < n_iter) v += B.dot(o1, s1 & 3, min(b1, p.nb - 1) * 256, xl);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        v = butterfly_sum<64>(v);
         if (lane == 0) r.y[lu] = f32_to_f16_bits(v);
     }
 }
@@ -523,7 +531,7 @@ __device__ __forceinline__ void kq_multi_first_packed(const KqMultiParams &p, in
     lds_barrier();
     if (u0 < p.n_units) {
         float v = S.dot(boff, u, b * 256, xl);
-        for (int o = p.slots >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        v = kq_row_sum(v, p.slots);
         if (slot == 0 && sub < n) r.y[r0 + sub] = f32_to_f16_bits(v);
     }
     kq_multi_units(p, u0 + gridDim.x * 4, lane, xl);

@@ -136,6 +136,32 @@ __device__ __forceinline__ float sum_xor_rows(float x) {
     return a + b;
 }
 
+// v + v[lane ^ q] for q = W/2, W/4, ..., 1 (the __shfl_xor butterfly over
+// aligned groups of W = 32 or 64 lanes; every lane ends with its group's
+// sum), on the VALU: the xor-32 / xor-16 steps by row swaps, then DPP
+// rotations within 16-lane rows.  After the steps above q, lanes whose
+// indices differ only in bits above q's hold equal values, and row_ror:q
+// reaches lane (l + q) mod 16, which differs from l ^ q only in those
+// bits, so every step adds the same two values, in the same order, as the
+// shuffle butterfly: the results are bit-identical.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_add(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+    return v + __builtin_bit_cast(float, moved);
+}
+
+template <int W>
+__device__ __forceinline__ float butterfly_sum(float v) {
+    static_assert(W == 32 || W == 64, "groups of 32 or 64 lanes");
+    if constexpr (W == 64) v = sum_xor_rows<32>(v);
+    v = sum_xor_rows<16>(v);
+    v = dpp_row_add<0x128>(v);  // row_ror:8
+    v = dpp_row_add<0x124>(v);  // row_ror:4
+    v = dpp_row_add<0x122>(v);  // row_ror:2
+    v = dpp_row_add<0x121>(v);  // row_ror:1
+    return v;
+}
+
 // Workgroup barrier without the fence of __syncthreads (which waits for all
 // outstanding vector memory operations); callers wait for what they need.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
