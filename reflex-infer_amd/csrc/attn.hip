@@ -245,8 +245,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
             float mx = -INFINITY;
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) mx = fmaxf(mx, sc[buf][sm_h][l32 + 32 * jj]);
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+            mx = butterfly_max<32>(mx);  // the head's 32 lanes are all active
             const float m_old = stat[0][sm_h];
             const float m_new = fmaxf(m_old, mx);
             // m_new is finite: the tile holds at least one position.
@@ -259,8 +258,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnParams p) {
                 sum += e;
                 sc[buf][sm_h][j] = I8 && p0 + j < end ? e * T.vs[jj] : e;
             }
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+            sum = butterfly_sum<32>(sum);  // the __shfl_xor butterfly's values, on the VALU
             // The 32 threads of a head are in one wave: their reads of stat
             // above precede this write.
             if (l32 == 0) {
@@ -397,14 +395,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnParams p) {
     if (wv == 0) {
         const bool ok = lane < p.n_chunks;
         if (!ok) m = -INFINITY;
-        // max over the 64 lanes (exact in any order): row swaps, then DPP
-        // rotations within 16-lane rows (no LDS instruction)
-        float M = max_xor_rows<32>(m);
-        M = max_xor_rows<16>(M);
-        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x128, 0xF, 0xF, false)));
-        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x124, 0xF, 0xF, false)));
-        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x122, 0xF, 0xF, false)));
-        M = fmaxf(M, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, M), 0x121, 0xF, 0xF, false)));
+        // max over the 64 lanes (exact in any order), no LDS instruction
+        const float M = butterfly_max<64>(m);
         const float e = ok ? expf(m - M) : 0.0f;
         wgt[lane] = e;
         // Butterfly sum: a fixed association (every lane gets the same

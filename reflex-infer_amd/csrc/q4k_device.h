@@ -162,6 +162,26 @@ __device__ __forceinline__ float butterfly_sum(float v) {
     return v;
 }
 
+// The maximum over aligned groups of W = 32 or 64 lanes (exact in any
+// order), every lane getting it: row swaps, then DPP rotations.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_max(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false);
+    return fmaxf(v, __builtin_bit_cast(float, moved));
+}
+
+template <int W>
+__device__ __forceinline__ float butterfly_max(float v) {
+    static_assert(W == 32 || W == 64, "groups of 32 or 64 lanes");
+    if constexpr (W == 64) v = max_xor_rows<32>(v);
+    v = max_xor_rows<16>(v);
+    v = dpp_row_max<0x128>(v);
+    v = dpp_row_max<0x124>(v);
+    v = dpp_row_max<0x122>(v);
+    v = dpp_row_max<0x121>(v);
+    return v;
+}
+
 // Workgroup barrier without the fence of __syncthreads (which waits for all
 // outstanding vector memory operations); callers wait for what they need.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
