@@ -112,7 +112,9 @@ hipError_t launch_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, int
     const int64_t threads = (int64_t)n_ids * (K >> 4);
     const int64_t grid = (threads + 255) / 256;
     if (grid <= 0) return hipSuccess;
-    if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
+    // the contiguous-store kernels form the wave index blockIdx.x * 4 + w in
+    // 32 bits (2^30 workgroups: 16 TB of output, far past any device)
+    if (grid > (int64_t)1 << 30) return hipErrorInvalidValue;
     // 8-output groups per thread: 4 (stores contiguous across the wave in
     // 512-output runs) when K allows, else 2, or 2 adjacent ones
     if (K % 2048 == 0)
