@@ -680,8 +680,12 @@ hipError_t launch_kq_multi(const GemvRange *ranges, const int *types, int n_rang
 // Q6_K rows (reference dequant_embedding_q6k_kernel, q4_gemm.cu:574-616): a
 // thread writes 8 consecutive outputs of one row with one 16-byte store;
 // w = d*sc*(q - 32) is exact in fp32, so the fp16 result is bit-identical.
-// Nontemporal stores, as the Q4_K gather.
-template <bool kBatched>
+// Nontemporal stores, as the Q4_K gather.  kUniform (K a multiple of
+// 1024): a row's K/16 threads are whole waves, so the row index, the id (a
+// scalar load) and the row's buffer resource are wave-uniform; otherwise the
+// resource comes from a per-lane id and every buffer load runs in a
+// readfirstlane loop over the wave's distinct rows.
+template <bool kBatched, bool kUniform>
 __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ dst,
                                                         const uint8_t *__restrict__ w,
                                                         const int32_t *__restrict__ ids,
@@ -690,7 +694,13 @@ __global__ __launch_bounds__(256) void embed_q6k_kernel(uint16_t *__restrict__ d
     constexpr int BYTES = KqFormat<14>::kBytes;
     const int per_row = K >> 4;  // 16-value sub-blocks (one int8 scale each)
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t i = t / per_row;
+    int64_t i;
+    if (kUniform) {
+        const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4u + (threadIdx.x >> 6)));
+        i = (int64_t)(wave / (uint32_t)(per_row >> 6));
+    } else {
+        i = t / per_row;
+    }
     const int c = (int)(t - i * per_row);
     if (i >= n_ids) return;
     u32x4 *out = reinterpret_cast<u32x4 *>(dst + i * K + c * 16);
@@ -746,11 +756,19 @@ hipError_t launch_kq_embed(uint16_t *dst, const uint8_t *w, const int32_t *ids, 
                            int64_t n_vocab, int n_ids, int K, hipStream_t st) {
     const int64_t threads = (int64_t)n_ids * (K / 16);
     const int64_t grid = (threads + 255) / 256;
-    if (grid > 0x7FFFFFFF) return hipErrorInvalidValue;
-    if (ids)
-        embed_q6k_kernel<true><<<(unsigned)grid, 256, 0, st>>>(dst, w, ids, 0, n_vocab, n_ids, K);
-    else
-        embed_q6k_kernel<false><<<(unsigned)grid, 256, 0, st>>>(dst, w, nullptr, token_id, 0, 1, K);
+    // the uniform kernel forms the wave index blockIdx.x * 4 + w in 32 bits
+    if (grid > (int64_t)1 << 30) return hipErrorInvalidValue;
+    const bool uniform = (K / 16) % 64 == 0;
+    if (ids) {
+        if (uniform)
+            embed_q6k_kernel<true, true><<<(unsigned)grid, 256, 0, st>>>(dst, w, ids, 0, n_vocab, n_ids, K);
+        else
+            embed_q6k_kernel<true, false><<<(unsigned)grid, 256, 0, st>>>(dst, w, ids, 0, n_vocab, n_ids, K);
+    } else if (uniform) {
+        embed_q6k_kernel<false, true><<<(unsigned)grid, 256, 0, st>>>(dst, w, nullptr, token_id, 0, 1, K);
+    } else {
+        embed_q6k_kernel<false, false><<<(unsigned)grid, 256, 0, st>>>(dst, w, nullptr, token_id, 0, 1, K);
+    }
     return hipGetLastError();
 }
 
