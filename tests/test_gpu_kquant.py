@@ -151,6 +151,30 @@ def test_q6k_embedding_bit_exact(K):
     assert np.array_equal(host16(out), orc.kq_embed_rows_f16(Wn, K, 14, ids))
 
 
+def test_q6k_embedding_full_table_zipf():
+    """The Q6_K gather at BASELINE configs[4]'s size: a [151936 x 2048] table
+    of ggml-quantised N(0, 0.02) weights (rows of 1680 bytes), 4096 Zipf(1.1)
+    ids over the whole vocabulary plus the last row and two out-of-range ids,
+    bit-exact against the oracle's dequantisation of the addressed rows (the
+    kernel's wave-uniform-row form: the K / 16 threads of a row are whole
+    waves)."""
+    vocab, K = 151936, 2048
+    g = torch.Generator(device="cuda").manual_seed(48)
+    src = torch.randn((vocab, K), generator=g, device="cuda") * 0.02
+    table = capi.quantize_ggml(src, 14)
+    del src
+    ids = util.zipf_ids(49, 4096, vocab)
+    ids[-1] = vocab - 1
+    ids[5], ids[77] = -1, vocab
+    out = torch.empty((ids.size, K), dtype=torch.float16, device="cuda")
+    capi.embed_rows_f16(out, table, vocab, dev(ids), K, ggml_type=14)
+    got = host16(out)
+    ref = orc.kq_embed_rows_f16(table.cpu().numpy(), K, 14, ids)
+    assert np.array_equal(got, ref)
+    assert not got[5].any() and not got[77].any()
+    assert np.unique(ids).size > 1000
+
+
 @pytest.mark.parametrize("t", [13, 14])
 # up to 16 tokens: the small-batch kernel (row tiles of 16 and 32); more:
 # the MFMA GEMM (partial row and token tiles; the 64- and 40-row shapes split
